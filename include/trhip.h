@@ -1,0 +1,134 @@
+/*
+ * trhip.h -- C-ABI of libtrhip, the MI355X (gfx950) implementation of TR's quantized GGUF
+ * matmul. Plain integers and pointers only, so the Go runtime can bind it through purego
+ * or cgo. Reference citations are relative to the reference repository root; "tensor/"
+ * means internal/compute/tensor/ and "gpu/" means internal/compute/gpu/.
+ *
+ * Conventions
+ *  - Every entry point returns an int status (TRHIP_OK == 0). Nothing aborts and nothing
+ *    throws across the ABI. trhip_last_error(ctx) gives the detail text of the last
+ *    failure on that context; trhip_strerror(code) names a code.
+ *  - A context owns one device and one in-order HIP stream. Calls on one context must be
+ *    serialized by the caller (the reference takes one backend lock per call,
+ *    gpu/gpu.go:211-232). Work is asynchronous until trhip_sync / trhip_d2h.
+ *  - Weights are [N, K] quantized rows (blocks along K), activations x are fp32 [M, K]
+ *    row-major, outputs c are fp32 [M, N] row-major; x and c are device pointers from
+ *    trhip_alloc (or any device allocation on the context's device).
+ */
+#ifndef TRHIP_H
+#define TRHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. The reference reports coded panics (messages.New(H...)); out-of-memory is
+ * a catchable error there too (docs/spec/15_tensorler.md:528). */
+enum {
+    TRHIP_OK = 0,
+    TRHIP_ERR_INVALID = 1,     /* bad argument / shape / dtype                          */
+    TRHIP_ERR_OOM = 2,         /* device allocation failed                              */
+    TRHIP_ERR_HIP = 3,         /* HIP runtime error (name in trhip_last_error)          */
+    TRHIP_ERR_LAUNCH = 4,      /* kernel launch failed                                  */
+    TRHIP_ERR_UNSUPPORTED = 5, /* dtype not supported by this operator (e.g. act-quant q8) */
+    TRHIP_ERR_NO_DEVICE = 6,   /* no HIP device / driver                                */
+    TRHIP_ERR_BAD_SCALE = 7    /* NaN/Inf fp16 scale (H6686)                             */
+};
+
+/* Quantized dtypes; same block formats as tensor/quant.go:23-47 and gguf/types.go:31-41. */
+enum { TRHIP_Q8 = 1, TRHIP_Q4 = 2, TRHIP_Q4K = 3, TRHIP_Q6K = 4 };
+
+/* GEMV arithmetic for fp32 activations (trhip_gemm_q with M == 1).
+ * EXACT: bit-identical to TR's CPU quantDot (dequant + sdot32 order).
+ * FAST:  per-sub-block factored sums; within the north-star tolerance, not bit-identical. */
+enum { TRHIP_MODE_EXACT = 0, TRHIP_MODE_FAST = 1 };
+
+typedef struct trhip_ctx trhip_ctx;
+typedef struct trhip_wstore trhip_wstore;
+
+const char *trhip_strerror(int code);
+const char *trhip_last_error(const trhip_ctx *ctx);
+int trhip_version(void);
+
+/* Replaces the lazy GPU backend set-up: tensor/device_registry.go:51 (RegisterLazyBackend),
+ * gpu/gpu.go:86-170 (Count, setupFn). */
+int trhip_device_count(int *count);
+int trhip_init(int device, trhip_ctx **out);
+int trhip_destroy(trhip_ctx *ctx);
+/* The context's stream as a hipStream_t (for callers that interleave their own work). */
+void *trhip_stream(trhip_ctx *ctx);
+
+/* Device memory; replaces Backend.Alloc and the loadHost/download pair
+ * (tensor/device.go:393, gpu/memory.go:524). */
+int trhip_alloc(trhip_ctx *ctx, size_t bytes, void **dptr);
+int trhip_free(trhip_ctx *ctx, void *dptr);
+int trhip_h2d_async(trhip_ctx *ctx, void *dst, const void *src, size_t bytes);
+int trhip_d2h(trhip_ctx *ctx, void *dst, const void *src, size_t bytes); /* waits */
+int trhip_memset_async(trhip_ctx *ctx, void *dst, int value, size_t bytes);
+int trhip_sync(trhip_ctx *ctx);
+
+/* Stream-ordered timing events (the reference's TR_GPU_PROFILE events, gpu/profile.go:1-34). */
+int trhip_event_create(trhip_ctx *ctx, void **ev);
+int trhip_event_record(trhip_ctx *ctx, void *ev);
+int trhip_event_elapsed_ms(void *ev_start, void *ev_end, float *ms);
+int trhip_event_destroy(void *ev);
+
+/* Load gate, tensor/quant.go:108-128 (CheckQuantScales): index of the first block with a
+ * NaN/Inf fp16 scale in *bad_block, or -1. Host-side, no device needed. */
+int trhip_check_quant_scales(int dtype, const void *raw, size_t raw_bytes, int64_t *bad_block);
+
+/* Device-resident weight store. Replaces RawBackend.FromRaw for quantized dtypes
+ * (tensor/typed.go:22-30, gpu/typed.go:24-35, tensor/quant.go:75-81): raw holds N*K/blk
+ * GGUF blocks in file order; they are uploaded asynchronously and repacked on the device
+ * into per-field planes (codes, scales) for 128-bit coalesced loads. No value is decoded.
+ * The host buffer must stay valid until the next trhip_sync on ctx. */
+int trhip_wstore_create(trhip_ctx *ctx, int dtype, const void *raw, size_t raw_bytes, int64_t N,
+                        int64_t K, trhip_wstore **out);
+int trhip_wstore_destroy(trhip_wstore *w); /* Releaser.Release, tensor/device.go:520-522 */
+int trhip_wstore_info(const trhip_wstore *w, int *dtype, int64_t *N, int64_t *K, size_t *device_bytes);
+/* RawBackend.ToRaw (tensor/typed.go:27): the original GGUF bytes of rows [row0, row0+rows). */
+int trhip_wstore_to_raw(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t rows, void *raw_out);
+
+/* Backend.Gemm / GemmSet for a quantized right operand (tensor/device.go:478,
+ * tensor/device_registry.go:193-195, tensor/cpu_dtype.go:448-466, gpu/backend_quant.go:43-65):
+ *   c[m, n] (+)= sum_k x[m, k] * deq(w)[row0 + n, k],  m < M, n < N, k < K.
+ * accumulate != 0 is Gemm (c +=), 0 is GemmSet (c =). K must equal the store's K and
+ * row0 + N <= store N (row slices, tensor/quant.go:266-272). M == 1 is the decode GEMV
+ * (tensor/cpu_quant.go:151); M > 1 follows quantGemmPanels' 256-deep chunk order
+ * (tensor/cpu_quant.go:103-147). K == 0 is the empty sum (c unchanged, zeroed when
+ * accumulate == 0). mode: TRHIP_MODE_EXACT or TRHIP_MODE_FAST (M == 1 only). */
+int trhip_gemm_q(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x,
+                 float *c, int64_t M, int64_t K, int accumulate, int mode);
+
+/* ActQuantGemmer.GemmActQuant (tensor/matmul.go:59-61, tensor/cpu_dtype.go:438-446 ->
+ * tensor/cpu_quant_q8.go:125-259): x rows are quantized on the device to Q8 blocks of the
+ * weight's block size (quantizeQ8), integer block sums run on int8 MFMA, and the per-block
+ * fp32 epilogue follows the reference order, so outputs are bit-identical to the CPU path.
+ * Rows holding NaN/Inf use the fp32 path for that row only. dtype must be q4, q4_k or q6_k
+ * (QuantActSupported, tensor/cpu_quant_q8.go:122), else TRHIP_ERR_UNSUPPORTED. */
+int trhip_gemm_q_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x,
+                      float *c, int64_t M, int64_t K, int accumulate);
+
+/* QuantOpener.OpenQuant (tensor/quant.go:103-105, gpu/backend_quant.go:117-134): elements
+ * [elem_off, elem_off+n) of the store in row-major order, dequantized to fp32, bit-identical
+ * to tensor/quant.go:139-205. elem_off and n must be multiples of the block size. */
+int trhip_open_q(trhip_ctx *ctx, const trhip_wstore *w, int64_t elem_off, int64_t n, float *out);
+
+/* Backend.Embedding for a quantized table (tensor/device.go:482, tensor/cpu_quant.go:163-171):
+ * out[i, :] = deq(w)[idx[i], :]; idx is a device array of nidx int64 row indices. Indices are
+ * checked on the device; an out-of-range index returns TRHIP_ERR_INVALID (H3043). */
+int trhip_embedding_q(trhip_ctx *ctx, const trhip_wstore *w, const int64_t *idx, int64_t nidx, float *out);
+
+/* Quantize fp32 rows to Q8 activation blocks on the device (tensor/cpu_quant_q8.go:39-68):
+ * q [M, K] int8, d [M, K/blk] fp32, bs [M, K/16] int16; blk is 32 or 256. Exposed for
+ * parity tests and for callers that reuse one quantized activation across weights. */
+int trhip_quantize_q8(trhip_ctx *ctx, const float *x, int64_t M, int64_t K, int blk, int8_t *q, float *d,
+                      int16_t *bs);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

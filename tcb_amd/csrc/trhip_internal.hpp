@@ -1,0 +1,151 @@
+// trhip_internal.hpp -- shared definitions of libtrhip (gfx950 only).
+//
+// Device layout of a weight store ("planes"). GGUF blocks are uploaded unchanged and then
+// repacked on the device, field by field, so that every plane is 16-byte aligned and a lane's
+// bytes for one block are contiguous. Nothing is decoded; the repack is a byte permutation and
+// trhip_wstore_to_raw inverts it exactly. Per row of nb blocks:
+//
+//   q8   : qs [N][nb][32]  int8 codes (block order)          d [N][nb] fp16
+//   q4   : qs [N][nb][16]  packed nibbles (block order)       d [N][nb] fp16
+//   q4_k : hdr[N][nb][16]  d, dmin, scales[12] (block order)  qs[N][nb][128] lane-sliced (see below)
+//   q6_k : ql [N][nb][128] lane-sliced   qh [N][nb][64] lane-sliced   sc [N][nb][16]   d [N][nb] fp16
+//
+// Lane slicing: the exact GEMV gives each of the 4 lanes of a row 8 consecutive elements of every
+// 32-element group (lane t owns sdot32 accumulator t, tensor/cpu_gemv_amd64.s:190-213). The bytes a
+// lane needs are moved next to each other:
+//   q4_k qs  : new[32t + 8g + l]        = old[32g + 8t + l]            (g < 4, l < 8)
+//   q6_k ql  : new[32t + 16n + 8h + l]  = old[64n + 32h + 8t + l]      (n, h < 2, l < 8)
+//   q6_k qh  : new[16t + 8n + l]        = old[32n + 8t + l]            (n < 2, l < 8)
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include <mutex>
+#include <string>
+
+#include "../../include/trhip.h"
+
+namespace trhip {
+
+constexpr int kQ8 = TRHIP_Q8, kQ4 = TRHIP_Q4, kQ4K = TRHIP_Q4K, kQ6K = TRHIP_Q6K;
+
+__host__ __device__ constexpr int block_elems(int dt) { return (dt == kQ8 || dt == kQ4) ? 32 : 256; }
+__host__ __device__ constexpr int block_bytes(int dt) {  // tensor/quant.go:23-29
+    return dt == kQ8 ? 34 : dt == kQ4 ? 18 : dt == kQ4K ? 144 : 210;
+}
+
+// Planes of one store (all pointers are device pointers into one allocation).
+struct Planes {
+    const uint8_t *qs;   // q8/q4 codes, q4_k qs, q6_k ql
+    const uint8_t *aux;  // q4_k hdr, q6_k qh
+    const uint8_t *sc;   // q6_k scales
+    const uint16_t *d;   // q8/q4/q6_k fp16 scale
+    int64_t nb;          // blocks per row
+};
+
+// Bytes per block in each plane.
+__host__ __device__ constexpr int qs_bytes(int dt) { return dt == kQ8 ? 32 : dt == kQ4 ? 16 : 128; }
+__host__ __device__ constexpr int aux_bytes(int dt) { return dt == kQ4K ? 16 : dt == kQ6K ? 64 : 0; }
+__host__ __device__ constexpr int sc_bytes(int dt) { return dt == kQ6K ? 16 : 0; }
+__host__ __device__ constexpr int d_bytes(int dt) { return dt == kQ4K ? 0 : 2; }
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {  // exact for finite values and +-Inf
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// Byte k (0..3) of a dword as float: v_cvt_f32_ubyte{k}.
+__device__ __forceinline__ float ubyte_f(uint32_t v, int k) { return (float)((v >> (8 * k)) & 0xFFu); }
+
+// q4_k scale/min unpack for all 8 sub-blocks from the 12 scale bytes (tensor/quant.go:158-163),
+// done four bytes at a time. sc[j], m[j] are returned as 4 packed bytes each (j < 4, j >= 4).
+__device__ __forceinline__ void q4k_scales(uint32_t s0, uint32_t s1, uint32_t s2, uint32_t &sc_lo,
+                                           uint32_t &sc_hi, uint32_t &m_lo, uint32_t &m_hi) {
+    sc_lo = s0 & 0x3F3F3F3Fu;
+    m_lo = s1 & 0x3F3F3F3Fu;
+    sc_hi = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+    m_hi = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
+}
+
+// Element k of weight row `row`, dequantized exactly as tensor/quant.go:139-205 (scalar, slow;
+// used where one element at a time is needed).
+template <int DT>
+__device__ __forceinline__ float deq_at(const Planes p, int64_t row, int64_t k) {
+    constexpr int be = block_elems(DT);
+    int64_t bi = row * p.nb + k / be;
+    int e = (int)(k % be);
+    if (DT == kQ8) {
+        return (float)(int8_t)p.qs[bi * 32 + e] * f16_to_f32(p.d[bi]);
+    } else if (DT == kQ4) {
+        uint8_t b = p.qs[bi * 16 + (e & 15)];
+        int code = (e < 16) ? (b & 0xF) : (b >> 4);
+        return (float)(code - 8) * f16_to_f32(p.d[bi]);
+    } else if (DT == kQ4K) {
+        const uint8_t *h = p.aux + bi * 16;
+        int j = e >> 5, g = e >> 6, ee = e & 31;
+        const uint8_t *s = h + 4;
+        uint8_t scv, mv;
+        if (j < 4) { scv = s[j] & 63; mv = s[j + 4] & 63; }
+        else { scv = (uint8_t)((s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4)); mv = (uint8_t)((s[j + 4] >> 4) | ((s[j] >> 6) << 4)); }
+        float d = f16_to_f32((uint16_t)(h[0] | (h[1] << 8))), dmin = f16_to_f32((uint16_t)(h[2] | (h[3] << 8)));
+        uint8_t b = p.qs[bi * 128 + 32 * (ee >> 3) + 8 * g + (ee & 7)];
+        int code = (j & 1) ? (b >> 4) : (b & 0xF);
+        return (d * (float)scv) * (float)code - dmin * (float)mv;
+    } else {
+        int n = e >> 7, k4 = (e >> 5) & 3, ee = e & 31;
+        uint8_t lo = p.qs[bi * 128 + 32 * (ee >> 3) + 16 * n + 8 * (k4 & 1) + (ee & 7)];
+        uint8_t hb = p.aux[bi * 64 + 16 * (ee >> 3) + 8 * n + (ee & 7)];
+        int nib = (k4 < 2) ? (lo & 0xF) : (lo >> 4);
+        int code = nib | (((hb >> (2 * k4)) & 3) << 4);
+        int8_t scv = (int8_t)p.sc[bi * 16 + 8 * n + 2 * k4 + ee / 16];
+        return f16_to_f32(p.d[bi]) * (float)scv * (float)(code - 32);
+    }
+}
+
+}  // namespace trhip
+
+// Host-side objects.
+struct trhip_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    // Grow-only device workspace (activation copies, quantized activations).
+    void *ws = nullptr;
+    size_t ws_bytes = 0;
+    int sm_count = 0;
+};
+
+struct trhip_wstore {
+    trhip_ctx *ctx = nullptr;
+    int dtype = 0;
+    int64_t N = 0, K = 0, nb = 0;
+    uint8_t *base = nullptr;  // one device allocation
+    size_t bytes = 0;
+    uint8_t *qs = nullptr, *aux = nullptr, *sc = nullptr;
+    uint16_t *d = nullptr;
+    trhip::Planes planes() const { return trhip::Planes{qs, aux, sc, d, nb}; }
+};
+
+namespace trhip {
+// Error helpers (api.hip).
+int fail(trhip_ctx *ctx, int code, const std::string &msg);
+int hip_fail(trhip_ctx *ctx, hipError_t e, const char *what);
+int launch_check(trhip_ctx *ctx, const char *what);
+void *workspace(trhip_ctx *ctx, size_t bytes, int *status);
+
+// Kernel launchers (one per source file). All return TRHIP_OK or an error code.
+int launch_repack(trhip_ctx *ctx, trhip_wstore *w, const uint8_t *raw_dev);
+int launch_unpack(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t rows, uint8_t *raw_dev);
+int launch_dequant(trhip_ctx *ctx, const trhip_wstore *w, int64_t block0, int64_t nblocks, float *out);
+int launch_embedding(trhip_ctx *ctx, const trhip_wstore *w, const int64_t *idx, int64_t nidx, float *out,
+                     int *bad_dev);
+int launch_gemv(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
+                bool acc, int mode);
+int launch_gemm_rows(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
+                     int64_t M, bool acc);
+int launch_quantize_q8(trhip_ctx *ctx, const float *x, int64_t M, int64_t K, int blk, int8_t *q, float *d,
+                       int16_t *bs, int32_t *flags);
+int launch_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
+                int64_t M, bool acc, const int8_t *q, const float *d, const int16_t *bs, const int32_t *flags);
+}  // namespace trhip

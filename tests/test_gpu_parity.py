@@ -1,0 +1,295 @@
+"""GPU parity: libtrhip through its C-ABI against the CPU oracle on the same seeded inputs.
+
+Bit-exact wherever the reference's arithmetic is fixed: dequantization (tensor/quant.go:139-205),
+the fp32 GEMV (quantDot = dequant + sdot32), the M>1 chunk order (quantGemmPanels), quantizeQ8 and
+the act-quant block kernels (cpu_quant_q8.go Go twins). Shapes follow the reference's own tests
+(cpu_quant_test.go, cpu_quant_q8_test.go, gpu/behavior_quant_test.go) plus the Llama-3-8B shapes.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import rel_err, same_bits
+from tcb_amd import BLOCK, MODE_EXACT, MODE_FAST, Q4, Q4K, Q6K, Q8, TrhipError
+from tcb_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+DTS = [Q8, Q4, Q4K, Q6K]
+ACT_DTS = [Q4, Q4K, Q6K]
+
+
+def _rng(seed):
+    return np.random.default_rng(seed)
+
+
+def _x(rng, n, scale=1.0):
+    return (rng.standard_normal(n) * scale).astype(np.float32)
+
+
+def _weights(dt, N, K, seed):
+    return O.small_scale_quant(dt, seed, N * K // BLOCK[dt][0])
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_store_round_trip(backend, dt):
+    """ToRaw gives the uploaded GGUF bytes back (the repack is a byte permutation)."""
+    N, K = 37, 2 * BLOCK[dt][0] * 4
+    raw = O.random_quant(dt, 99, N * K // BLOCK[dt][0])
+    w = backend.FromQuantized(dt, raw, N, K)
+    assert np.array_equal(w.ToRaw(), raw)
+    rb = raw.size // N
+    assert np.array_equal(w.ToRaw(5, 11), raw[5 * rb:16 * rb])
+    w.release()
+
+
+@pytest.mark.parametrize("dt,seed,want,at,sample", [
+    (Q8, 1, 0x9994d70c2568f054, 33, 0x3a0c6000),
+    (Q4K, 2, 0x9aea8c1a1a939707, 300, 0xc8f6bd40),
+    (Q6K, 3, 0xf982bdb0f96cd2fc, 300, 0xc02c0000),
+    (Q4, 4, 0xbe538ba4bf9b8554, 49, 0x3f328000),
+])
+def test_open_quant_golden(backend, dt, seed, want, at, sample):
+    """OpenQuant on the card reproduces the reference's llama.cpp golden hashes (quant_test.go:55-86)."""
+    elems = BLOCK[dt][0]
+    raw = O.random_quant(dt, seed, 512)
+    w = backend.FromQuantized(dt, raw, 512, elems)
+    out = backend.ctx.alloc(512 * elems * 4)
+    backend.OpenQuant(out, w)
+    y = out.download(np.float32, 512 * elems)
+    assert O.fnv(y) == want
+    assert y.view(np.uint32)[at] == sample
+    # block-aligned sub-range
+    out2 = backend.ctx.alloc(3 * elems * 4)
+    backend.OpenQuant(out2, w, offset=7 * elems, n=3 * elems)
+    same_bits(out2.download(np.float32, 3 * elems), y[7 * elems:10 * elems])
+    for b in (out, out2):
+        b.free()
+    w.release()
+
+
+def _gemv_case(backend, dt, N, K, seed, accumulate=True, row0=0, rows=None, x_off=0, scale=1.0):
+    rng = _rng(seed)
+    raw = _weights(dt, N, K, seed)
+    w = backend.FromQuantized(dt, raw, N, K)
+    rows = N - row0 if rows is None else rows
+    x = _x(rng, K, scale)
+    c0 = _x(rng, rows)
+    xb = backend.ctx.alloc(K * 4 + 64)
+    xb.upload(x, byte_offset=x_off)
+    cb = backend.ctx.to_device(c0)
+    if accumulate:
+        backend.Gemm(1, rows, K, (xb, x_off), w, cb, row0=row0)
+    else:
+        backend.GemmSet(1, rows, K, (xb, x_off), w, cb, row0=row0)
+    got = cb.download(np.float32, rows)
+    rb = raw.size // N
+    want = O.quant_gemm(dt, 1, rows, K, x, raw[row0 * rb:(row0 + rows) * rb], c0 if accumulate else None)
+    for b in (xb, cb):
+        b.free()
+    w.release()
+    return got, want.reshape(-1)
+
+
+@pytest.mark.parametrize("dt", DTS)
+@pytest.mark.parametrize("N,Kb", [(1, 1), (7, 1), (9, 3), (16, 5), (33, 11), (130, 16)])
+def test_gemv_exact_bits(backend, dt, N, Kb):
+    """M == 1, fp32 activations: bit-identical to quantDot (TestQuantGemvMatchesOpened shapes)."""
+    got, want = _gemv_case(backend, dt, N, Kb * BLOCK[dt][0], seed=N * 31 + Kb)
+    same_bits(got, want)
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_gemv_exact_large_inputs(backend, dt):
+    """x scaled by 1000 (TestQ8KernelsMatchGo's x1000 trials) stays bit-identical."""
+    got, want = _gemv_case(backend, dt, 64, 2560 if dt in (Q8, Q4) else 2560, seed=5, scale=1000.0)
+    same_bits(got, want)
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_gemv_set_slice_unaligned(backend, dt):
+    """GemmSet overwrites; a row slice reads its own rows; an unaligned x is copied first."""
+    K = 4 * BLOCK[dt][0]
+    got, want = _gemv_case(backend, dt, 50, K, seed=7, accumulate=False)
+    same_bits(got, want)
+    got, want = _gemv_case(backend, dt, 50, K, seed=8, row0=10, rows=20)
+    same_bits(got, want)
+    got, want = _gemv_case(backend, dt, 50, K, seed=9, x_off=4)
+    same_bits(got, want)
+
+
+@pytest.mark.parametrize("dt,N,K", [(Q4K, 14336, 4096), (Q4K, 4096, 14336), (Q6K, 1024, 4096), (Q8, 4096, 4096),
+                                    (Q4, 14336, 4096)])
+def test_gemv_llama_shapes_bits(backend, dt, N, K):
+    """Llama-3-8B shapes with encoded N(0, 0.02) weights (1% outliers for K-quants): bit-identical."""
+    raw = synth.quant_weights(dt, N, K, seed=11, outliers=0.01 if dt in (Q4K, Q6K) else 0.0)
+    x = synth.activations(1, K, seed=12)
+    w = backend.FromQuantized(dt, raw, N, K)
+    xb, cb = backend.ctx.to_device(x), backend.ctx.alloc(N * 4)
+    backend.GemmSet(1, N, K, xb, w, cb)
+    got = cb.download(np.float32, N)
+    want = O.quant_gemm(dt, 1, N, K, x, raw).reshape(-1)
+    same_bits(got, want)
+    for b in (xb, cb):
+        b.free()
+    w.release()
+
+
+def test_gemv_empty_sum(backend):
+    """K == 0: c unchanged for Gemm, zeroed for GemmSet (TestQuantGemvEdges)."""
+    w = backend.FromQuantized(Q8, np.zeros(0, np.uint8), 3, 0)
+    c = backend.ctx.to_device(np.array([1, 2, 3], np.float32))
+    xb = backend.ctx.alloc(16)
+    backend.Gemm(1, 3, 0, xb, w, c)
+    assert list(c.download(np.float32, 3)) == [1, 2, 3]
+    backend.GemmSet(1, 3, 0, xb, w, c)
+    assert list(c.download(np.float32, 3)) == [0, 0, 0]
+
+
+@pytest.mark.parametrize("dt", DTS)
+@pytest.mark.parametrize("M,N,K", [(2, 40, 256), (3, 70, 512), (9, 33, 1024), (17, 20, 2560)])
+def test_gemm_rows_bits(backend, dt, M, N, K):
+    """M > 1, fp32 activations: bit-identical to quantGemmPanels' 256-chunk order (TestQuantMatMulSameBitsAsOpened)."""
+    rng = _rng(M * 7 + N)
+    raw = _weights(dt, N, K, N + K)
+    w = backend.FromQuantized(dt, raw, N, K)
+    x = _x(rng, M * K)
+    c0 = _x(rng, M * N)
+    xb, cb = backend.ctx.to_device(x), backend.ctx.to_device(c0)
+    backend.Gemm(M, N, K, xb, w, cb)
+    same_bits(cb.download(np.float32, M * N), O.quant_gemm(dt, M, N, K, x, raw, c0))
+    for b in (xb, cb):
+        b.free()
+    w.release()
+
+
+def _edge_rows(K, blk):
+    tiny = np.array([0x00400000], np.uint32).view(np.float32)[0]
+    rows = []
+    rows.append(np.zeros(K, np.float32))  # zero block
+    r = np.full(K, 3.0, np.float32)
+    r[1::2] = -3.0
+    rows.append(r)  # saturating +-127
+    r = np.full(K, 1e-3, np.float32)
+    r[5] = 1000.0
+    rows.append(r)  # single large
+    r = np.zeros(K, np.float32)
+    r[0], r[1], r[2] = tiny, -tiny / 2, tiny / 4
+    rows.append(r)  # 127/amax overflows
+    r = np.full(K, 0.5, np.float32)
+    r[0] = 1.0
+    rows.append(r)  # RNE tie 63.5 -> 64
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("blk", [32, 256])
+def test_quantize_q8_bits(backend, blk):
+    """Device quantizeQ8 == cpu_quant_q8.go:39-68 bit for bit (random rows and the edge blocks)."""
+    K = 1024
+    rng = _rng(blk)
+    X = np.concatenate([_edge_rows(K, blk), (rng.standard_normal((6, K)) * np.array([1, 1000, 1e-30, 1, 7, 1e20])[:, None]).astype(np.float32)])
+    M = X.shape[0]
+    xb = backend.ctx.to_device(X)
+    qb, db, bb = backend.ctx.alloc(M * K), backend.ctx.alloc(M * K // blk * 4), backend.ctx.alloc(M * K // 16 * 2)
+    backend.QuantizeQ8(xb, M, K, blk, qb, db, bb)
+    q = qb.download(np.int8, M * K).reshape(M, K)
+    d = db.download(np.float32, M * K // blk).reshape(M, -1)
+    bs = bb.download(np.int16, M * K // 16).reshape(M, -1)
+    for m in range(M):
+        wq, wd, wbs = O.quantize_q8(X[m], blk)
+        assert np.array_equal(q[m], wq), m
+        same_bits(d[m], wd)
+        assert np.array_equal(bs[m], wbs), m
+    for b in (xb, qb, db, bb):
+        b.free()
+
+
+@pytest.mark.parametrize("dt", ACT_DTS)
+@pytest.mark.parametrize("M,N,K", [(1, 70, 512), (5, 7, 256), (9, 40, 2560), (13, 5, 9728), (4, 33, 512)])
+def test_actq_bits(backend, dt, M, N, K):
+    """GemmActQuant == quantGemmAct bit for bit (TestQ8FourRowsMatchOneRow / TestQ8EightRowsMatchOneRow shapes,
+    including x1000 rows, zero-block rows and +-1 rows)."""
+    rng = _rng(M * 131 + N * K)
+    raw = _weights(dt, N, K, 7 * M + N + K)
+    X = _x(rng, M * K).reshape(M, K)
+    for m in range(M):
+        if m % 5 == 1:
+            X[m] *= 1000
+        elif m % 5 == 2:
+            X[m, :BLOCK[dt][0]] = 0
+        elif m % 5 == 3:
+            X[m] = 1 - 2 * (np.arange(K) % 2)
+    w = backend.FromQuantized(dt, raw, N, K)
+    c0 = _x(rng, M * N)
+    xb, cb = backend.ctx.to_device(X), backend.ctx.to_device(c0)
+    backend.GemmActQuant(M, N, K, xb, w, cb)
+    same_bits(cb.download(np.float32, M * N), O.quant_gemm_act(dt, M, N, K, X, raw, c0))
+    for b in (xb, cb):
+        b.free()
+    w.release()
+
+
+@pytest.mark.parametrize("dt", ACT_DTS)
+@pytest.mark.parametrize("bad", [np.nan, np.inf, -np.inf])
+def test_actq_keeps_non_finite(backend, dt, bad):
+    """A row with NaN/Inf takes the fp32 path on its own; its neighbours are untouched (TestQ8PathKeepsNonFinite)."""
+    M, N, K = 5, 9, 512
+    rng = _rng(34)
+    raw = _weights(dt, N, K, M + N)
+    X = _x(rng, M * K).reshape(M, K)
+    X[2, K // 2] = bad
+    w = backend.FromQuantized(dt, raw, N, K)
+    xb, cb = backend.ctx.to_device(X), backend.ctx.alloc(M * N * 4)
+    backend.GemmActQuant(M, N, K, xb, w, cb, accumulate=False)
+    got = cb.download(np.float32, M * N).reshape(M, N)
+    same_bits(got, O.quant_gemm_act(dt, M, N, K, X, raw))
+    same_bits(got[2], O.quant_gemm(dt, 1, N, K, X[2], raw))
+    for b in (xb, cb):
+        b.free()
+    w.release()
+
+
+@pytest.mark.parametrize("dt,N,K,M", [(Q4K, 14336, 4096, 16), (Q4K, 4096, 14336, 8), (Q6K, 1024, 4096, 32),
+                                      (Q4, 4096, 4096, 16)])
+def test_actq_llama_shapes_bits(backend, dt, N, K, M):
+    raw = synth.quant_weights(dt, N, K, seed=21, outliers=0.01 if dt in (Q4K, Q6K) else 0.0)
+    X = synth.activations(M, K, seed=22)
+    w = backend.FromQuantized(dt, raw, N, K)
+    xb, cb = backend.ctx.to_device(X), backend.ctx.alloc(M * N * 4)
+    backend.GemmActQuant(M, N, K, xb, w, cb, accumulate=False)
+    same_bits(cb.download(np.float32, M * N), O.quant_gemm_act(dt, M, N, K, X, raw))
+    for b in (xb, cb):
+        b.free()
+    w.release()
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_embedding(backend, dt):
+    """Selected rows dequantized (TestQuantEmbedding); an out-of-range row is refused (H3043)."""
+    D = 512
+    raw = O.random_quant(dt, 9, 5 * D // BLOCK[dt][0])
+    w = backend.FromQuantized(dt, raw, 5, D)
+    idx = [4, 0, 4, 2]
+    out = backend.ctx.alloc(len(idx) * D * 4)
+    backend.Embedding(out, w, idx)
+    same_bits(out.download(np.float32, len(idx) * D), O.embedding(dt, raw, D, idx))
+    with pytest.raises(TrhipError):
+        backend.Embedding(out, w, [5])
+    out.free()
+    w.release()
+
+
+def test_actq_refuses_q8(backend):
+    w = backend.FromQuantized(Q8, O.random_quant(Q8, 1, 2), 2, 32)
+    xb, cb = backend.ctx.alloc(128), backend.ctx.alloc(8)
+    with pytest.raises(TrhipError) as e:
+        backend.GemmActQuant(1, 2, 32, xb, w, cb)
+    assert e.value.code == 5
+
+
+def test_store_refuses_bad_scale(backend):
+    raw = O.random_quant(Q8, 3, 3)
+    raw[34 + 1] = 0x7C  # block 1 scale -> +Inf
+    with pytest.raises(TrhipError) as e:
+        backend.FromQuantized(Q8, raw, 3, 32)
+    assert e.value.code == 7
