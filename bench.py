@@ -1,0 +1,218 @@
+#!/usr/bin/env python3
+"""Headline benchmark of libtrhip on one MI355X.
+
+Workload (the Q4_K decode GEMV the metric is quoted on): weight 14336 x 4096 Q4_K (Llama-3-8B gate/up
+shape), entries N(0, 0.02) with a seeded 1% scaled x10, encoded by tcb_amd.synth; x fp32 N(0, 1); batch 1;
+c = x . deq(W)^T (GemmSet). One step is one GEMV. The weights sit in a ring of copies larger than the
+256 MB MALL (>= 1.1 GiB), so each step streams its weight from HBM ("cold"); a warm figure (same copy
+every step) is reported beside it. The steps are captured once into a HIP graph and replayed, so host
+launch overhead does not enter the device timing; HIP events on the library's stream bracket the
+replays.
+
+Also reported: the act-quant prefill GEMM (Q4_K 14336 x 4096, M = 512 rows quantized to Q8 on the
+device, int32 block sums, fp32 epilogue) in int8 TOPS = 2*M*N*K / time, and the CPU baseline: the AVX2
+restatement of the reference's sdotq4k path (oracle/trq_avx2.c), all host cores, on the same bytes.
+
+Prints one JSON line. --gpus N > 1 exits: this build runs on one GPU.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "Q4_K GEMV µs + HBM GB/s (% peak) at 8B shapes; prefill GEMM int8 TOPS"
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, datasheet
+INT8_PEAK_TOPS = 5033.0      # MI355X dense int8 MFMA, datasheet (5.03 POPS)
+N, K = 14336, 4096
+RING_BYTES = int(1.1 * (1 << 30))
+
+
+def algorithmic_bytes(n, k):
+    # weights (144 B per 256-element block) + x (4K) + c written (4N)
+    return n * (k // 256) * 144 + 4 * k + 4 * n
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400, help="timed GEMVs (rounded up to whole ring passes)")
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--mode", choices=["exact", "fast"], default="fast",
+                    help="headline mode; the other mode is measured and reported beside it")
+    ap.add_argument("--prefill-m", type=int, default=512)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample (0 = skip)")
+    return ap.parse_args()
+
+
+def time_graph(tb, graph, replays):
+    from tcb_amd import _lib
+    L = _lib.lib()
+    ctx = tb.ctx
+    e0, e1 = ctx.event(), ctx.event()
+    ctx.record(e0)
+    for _ in range(replays):
+        rc = L.trhip_graph_launch(ctx.h, graph)
+        if rc:
+            raise RuntimeError("graph launch failed: %d" % rc)
+    ctx.record(e1)
+    ms = ctx.elapsed_ms(e0, e1)
+    for e in (e0, e1):
+        L.trhip_event_destroy(e)
+    return ms
+
+
+def capture(tb, body):
+    import ctypes
+    from tcb_amd import _lib
+    L = _lib.lib()
+    if L.trhip_graph_begin(tb.ctx.h):
+        raise RuntimeError("graph begin failed")
+    try:
+        body()
+    finally:
+        g = _lib.P()
+        rc = L.trhip_graph_end(tb.ctx.h, ctypes.byref(g))
+    if rc:
+        raise RuntimeError("graph end failed: %s" % L.trhip_last_error(tb.ctx.h))
+    return g
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print("bench.py: this build measures one MI355X; multi-GPU runs (--gpus %d) are not part of it." % a.gpus,
+              file=sys.stderr)
+        return 2
+    from tcb_amd import MODE_EXACT, MODE_FAST, Q4K, QuantBackend, _lib, synth
+
+    mode = MODE_FAST if a.mode == "fast" else MODE_EXACT
+    L = _lib.lib()
+    tb = QuantBackend(0)
+    ctx = tb.ctx
+
+    raw = synth.quant_weights(Q4K, N, K, seed=3, outliers=0.01)
+    x = synth.activations(1, K, seed=4)
+    wbytes = raw.nbytes
+    ring_n = max(2, -(-RING_BYTES // wbytes))
+    ring = [tb.FromQuantized(Q4K, raw, N, K) for _ in range(ring_n)]
+    xb = ctx.to_device(x)
+    cb = ctx.alloc(N * 4)
+
+    warm_replays = max(1, -(-a.warmup // ring_n))
+    replays = max(1, -(-a.steps // ring_n))
+    steps = replays * ring_n
+    abytes = algorithmic_bytes(N, K)
+
+    def measure(md):
+        # one eager call sizes any workspace before capture
+        tb.GemmSet(1, N, K, xb, ring[0], cb, mode=md)
+        ctx.sync()
+        out = cb.download(np.float32, N)
+        g_cold = capture(tb, lambda: [tb.GemmSet(1, N, K, xb, w, cb, mode=md) for w in ring])
+        g_warm = capture(tb, lambda: [tb.GemmSet(1, N, K, xb, ring[0], cb, mode=md) for _ in ring])
+        time_graph(tb, g_cold, warm_replays)
+        ms_cold = time_graph(tb, g_cold, replays)
+        time_graph(tb, g_warm, 1)
+        ms_warm = time_graph(tb, g_warm, replays)
+        for g in (g_cold, g_warm):
+            L.trhip_graph_destroy(g)
+        return out, ms_cold * 1e3 / steps, ms_warm * 1e3 / steps
+
+    gpu_out, us_cold, us_warm = measure(mode)
+    gbs_cold = abytes / (us_cold * 1e-6) / 1e9
+    gbs_warm = abytes / (us_warm * 1e-6) / 1e9
+    other = MODE_EXACT if mode == MODE_FAST else MODE_FAST
+    other_out, us_other, us_other_warm = measure(other)
+    exact_out = other_out if other == MODE_EXACT else gpu_out
+    other_name = "exact" if other == MODE_EXACT else "fast"
+
+    # prefill: act-quant GEMM, M rows, same weight
+    prefill = None
+    if a.prefill_m > 0:
+        M = a.prefill_m
+        X = synth.activations(M, K, seed=5)
+        Xb = ctx.to_device(X)
+        Cb = ctx.alloc(M * N * 4)
+        tb.GemmActQuant(M, N, K, Xb, ring[0], Cb, accumulate=False)
+        ctx.sync()
+        gp = capture(tb, lambda: tb.GemmActQuant(M, N, K, Xb, ring[0], Cb, accumulate=False))
+        time_graph(tb, gp, 3)
+        reps = 10
+        ms = time_graph(tb, gp, reps) / reps
+        L.trhip_graph_destroy(gp)
+        tops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+        prefill = {"workload": "act-quant GEMM q4_k %dx%d, M=%d (quantize + int block sums + fp32 epilogue)" % (N, K, M),
+                   "us": round(ms * 1e3, 2), "int8_tops": round(tops, 2),
+                   "frac_of_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+        Xb.free()
+        Cb.free()
+
+    # CPU baseline: AVX2 restatement of the reference's sdotq4k GEMV, all host cores, same bytes
+    cpu = None
+    if a.cpu_seconds > 0:
+        import ctypes
+        sys.path.insert(0, os.path.join(ROOT, "tests"))
+        import oracle as O
+        threads = len(os.sched_getaffinity(0))
+        copies = 16  # host ring of 16 weight copies (528 MB) so the sample streams from DRAM
+        hring = [raw.copy() for _ in range(copies)]
+        out = np.zeros(N, np.float32)
+        P = ctypes.c_void_p
+        xs = np.ascontiguousarray(x.reshape(-1))
+        O.lib().trq_avx2_quant_gemv(Q4K, N, K, xs.ctypes.data_as(P), hring[0].ctypes.data_as(P), out.ctypes.data_as(P), threads)
+        cpu_matches = bool(np.array_equal(out.view(np.uint32), exact_out.view(np.uint32)))
+        fast_out = gpu_out if mode == MODE_FAST else other_out
+        fast_err = float(np.max(np.abs(fast_out.astype(np.float64) - out) / (1.0 + np.abs(out.astype(np.float64)))))
+        n_done, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < a.cpu_seconds:
+            O.lib().trq_avx2_quant_gemv(Q4K, N, K, xs.ctypes.data_as(P), hring[n_done % copies].ctypes.data_as(P),
+                                        out.ctypes.data_as(P), threads)
+            n_done += 1
+        dt = time.perf_counter() - t0
+        cpu = {"value": round(abytes * n_done / dt / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+               "sample": "%d GEMVs of q4_k %dx%d over a 16-copy host ring, %.1f s; AVX2 sdotq4k restatement" % (
+                   n_done, N, K, dt),
+               "us_per_gemv": round(dt / n_done * 1e6, 1), "gpu_exact_bits_equal_cpu": cpu_matches,
+               "gpu_fast_max_rel_err_vs_cpu": fast_err}
+
+    line = {
+        "metric": METRIC,
+        "value": round(gbs_cold, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warm_replays * ring_n,
+        "ms_per_step": round(us_cold / 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "q4_k decode GEMV %dx%d batch 1, fp32 activations, %s mode, cold ring of %d copies (%.2f GiB)" % (
+            N, K, a.mode, ring_n, ring_n * wbytes / (1 << 30)), "N": N, "K": K, "batch": 1, "mode": a.mode},
+        "us_per_gemv": round(us_cold, 3),
+        "hbm_frac_of_peak": round(gbs_cold / HBM_PEAK_GBS, 4),
+        "warm": {"us_per_gemv": round(us_warm, 3), "GB/s": round(gbs_warm, 1)},
+        other_name + "_mode": {"us_per_gemv": round(us_other, 3), "GB/s": round(abytes / (us_other * 1e-6) / 1e9, 1),
+                               "warm_us_per_gemv": round(us_other_warm, 3)},
+        "roofline": {"bound": "hbm", "achieved": round(gbs_cold, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs_cold / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "gemv_q4_k_%s" % a.mode, "algorithmic_bytes_per_launch": abytes},
+        "prefill": prefill,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+    for w in ring:
+        w.release()
+    tb.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

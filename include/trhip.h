@@ -76,6 +76,16 @@ int trhip_event_record(trhip_ctx *ctx, void *ev);
 int trhip_event_elapsed_ms(void *ev_start, void *ev_end, float *ms);
 int trhip_event_destroy(void *ev);
 
+/* Stream capture into a replayable HIP graph (launch-bound sequences such as a decode sweep).
+ * Every call made on ctx between begin and end is recorded, not run; trhip_graph_launch replays it
+ * on the context's stream. Calls that would grow the context's workspace fail during capture: make
+ * one eager call of the same shapes first. Counterpart of the reference's CUDA-graph replay
+ * (gpu/graph.go); nothing on this path requires it. */
+int trhip_graph_begin(trhip_ctx *ctx);
+int trhip_graph_end(trhip_ctx *ctx, void **exec);
+int trhip_graph_launch(trhip_ctx *ctx, void *exec);
+int trhip_graph_destroy(void *exec);
+
 /* Load gate, tensor/quant.go:108-128 (CheckQuantScales): index of the first block with a
  * NaN/Inf fp16 scale in *bad_block, or -1. Host-side, no device needed. */
 int trhip_check_quant_scales(int dtype, const void *raw, size_t raw_bytes, int64_t *bad_block);

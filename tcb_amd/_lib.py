@@ -33,6 +33,10 @@ SIGNATURES = [
     ("trhip_event_record", INT, [P, P]),
     ("trhip_event_elapsed_ms", INT, [P, P, ctypes.POINTER(ctypes.c_float)]),
     ("trhip_event_destroy", INT, [P]),
+    ("trhip_graph_begin", INT, [P]),
+    ("trhip_graph_end", INT, [P, ctypes.POINTER(P)]),
+    ("trhip_graph_launch", INT, [P, P]),
+    ("trhip_graph_destroy", INT, [P]),
     ("trhip_check_quant_scales", INT, [INT, P, SZ, ctypes.POINTER(I64)]),
     ("trhip_wstore_create", INT, [P, INT, P, SZ, I64, I64, ctypes.POINTER(P)]),
     ("trhip_wstore_destroy", INT, [P]),

@@ -13,7 +13,8 @@
 //   q6_k: t = fl(d*fl(isum - 32*msum));        acc = fl(acc + fl(t*d8))              (:378-407)
 // blocks strictly in order. A row of x holding NaN/Inf takes the fp32 path (quantGemv) on its own
 // (cpu_quant_q8.go:186-194): the quantizer flags it and the kernel computes that row's outputs with
-// the exact fp32 dot (sdot32 order) instead.
+// the exact fp32 dot (sdot32 order) instead. The quantizer writes one flag byte per activation block
+// (plain stores, so no buffer has to be cleared first).
 #include "trhip_internal.hpp"
 
 namespace trhip {
@@ -22,7 +23,7 @@ namespace {
 template <int BLK>
 __global__ __launch_bounds__(256) void quantize_q8_kernel(const float *__restrict__ x, int64_t M, int64_t K,
                                                           int8_t *__restrict__ q, float *__restrict__ d,
-                                                          int16_t *__restrict__ bs, int32_t *__restrict__ flags) {
+                                                          int16_t *__restrict__ bs, uint8_t *__restrict__ bad_blk) {
     constexpr int TPB = BLK / 4;  // threads per activation block
     const int64_t nbk = K / BLK;
     const int64_t gt = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -31,7 +32,6 @@ __global__ __launch_bounds__(256) void quantize_q8_kernel(const float *__restric
     const int64_t gtc = live ? gt : total - 1;
     const int l4 = (int)(gtc % TPB);
     const int64_t blk_id = gtc / TPB;  // = m * nbk + b
-    const int64_t m = blk_id / nbk;
     const int64_t off = blk_id * BLK + 4 * l4;  // element offset in x (rows are contiguous: m*K + b*BLK)
     float4 v = *reinterpret_cast<const float4 *>(x + off);
     float a = 0.0f;
@@ -47,7 +47,7 @@ __global__ __launch_bounds__(256) void quantize_q8_kernel(const float *__restric
         bad |= __shfl_xor(bad, s);
     }
     if (!live) return;
-    if (bad && l4 == 0) atomicOr(flags + m, 1);
+    if (l4 == 0) bad_blk[blk_id] = (uint8_t)(bad != 0);
     float id = 127.0f / a;
     float dv;
     int c[4];
@@ -101,14 +101,16 @@ template <int DT, bool ACC>
 __global__ __launch_bounds__(256) void actq_valu_kernel(const Planes p, int64_t N, int64_t row0, int64_t K,
                                                         const float *__restrict__ x, const int8_t *__restrict__ q,
                                                         const float *__restrict__ d8, const int16_t *__restrict__ bs,
-                                                        const int32_t *__restrict__ flags, float *__restrict__ c) {
+                                                        const uint8_t *__restrict__ bad_blk, float *__restrict__ c) {
     const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t m = blockIdx.y;
     if (n >= N) return;
     const int64_t row = row0 + n;
     const int64_t nb = p.nb;
     float acc = 0.0f;
-    if (flags[m]) {
+    bool row_bad = false;
+    for (int64_t b = 0; b < nb; b++) row_bad |= bad_blk[m * nb + b] != 0;
+    if (row_bad) {
         acc = exact_dot_row<DT>(p, row, x + m * K, K);
     } else if (DT == kQ4) {
         const uint32_t *qa = reinterpret_cast<const uint32_t *>(q + m * K);
@@ -147,7 +149,7 @@ __global__ __launch_bounds__(256) void actq_valu_kernel(const Planes p, int64_t 
                 for (int t = 0; t < 4; t++)
 #pragma unroll
                     for (int hh = 0; hh < 2; hh++) {
-                        uint32_t wv = qw[8 * t + 2 * g + hh];
+                        uint32_t wv = qw[q4k_pos(32 * g + 8 * t + 4 * hh) / 4];
                         uint32_t nib = (j & 1) ? ((wv >> 4) & 0x0F0F0F0Fu) : (wv & 0x0F0F0F0Fu);
                         s = sdot4(nib, qa[64 * b + 8 * j + 2 * t + hh], s);
                     }
@@ -203,39 +205,39 @@ __global__ __launch_bounds__(256) void actq_valu_kernel(const Planes p, int64_t 
 
 template <int DT>
 int run_valu(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c, int64_t M,
-             bool acc, const int8_t *q, const float *d, const int16_t *bs, const int32_t *flags) {
+             bool acc, const int8_t *q, const float *d, const int16_t *bs, const uint8_t *bad) {
     dim3 grid((unsigned)((N + 255) / 256), (unsigned)M), block(256);
     if (acc)
-        hipLaunchKernelGGL((actq_valu_kernel<DT, true>), grid, block, 0, ctx->stream, w->planes(), N, row0, w->K, x, q, d, bs, flags, c);
+        hipLaunchKernelGGL((actq_valu_kernel<DT, true>), grid, block, 0, ctx->stream, w->planes(), N, row0, w->K, x, q, d, bs, bad, c);
     else
-        hipLaunchKernelGGL((actq_valu_kernel<DT, false>), grid, block, 0, ctx->stream, w->planes(), N, row0, w->K, x, q, d, bs, flags, c);
+        hipLaunchKernelGGL((actq_valu_kernel<DT, false>), grid, block, 0, ctx->stream, w->planes(), N, row0, w->K, x, q, d, bs, bad, c);
     return launch_check(ctx, "actq_valu");
 }
 
 }  // namespace
 
 int launch_quantize_q8(trhip_ctx *ctx, const float *x, int64_t M, int64_t K, int blk, int8_t *q, float *d, int16_t *bs,
-                       int32_t *flags) {
+                       uint8_t *bad) {
     if (M == 0 || K == 0) return TRHIP_OK;
     int64_t total = M * K / 4;
     dim3 grid((unsigned)((total + 255) / 256)), block(256);
     if (blk == 256)
-        hipLaunchKernelGGL(quantize_q8_kernel<256>, grid, block, 0, ctx->stream, x, M, K, q, d, bs, flags);
+        hipLaunchKernelGGL(quantize_q8_kernel<256>, grid, block, 0, ctx->stream, x, M, K, q, d, bs, bad);
     else
-        hipLaunchKernelGGL(quantize_q8_kernel<32>, grid, block, 0, ctx->stream, x, M, K, q, d, bs, flags);
+        hipLaunchKernelGGL(quantize_q8_kernel<32>, grid, block, 0, ctx->stream, x, M, K, q, d, bs, bad);
     return launch_check(ctx, "quantize_q8");
 }
 
 int launch_actq_mfma(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
-                     int64_t M, bool acc, const int8_t *q, const float *d, const int16_t *bs, const int32_t *flags);
+                     int64_t M, bool acc, const int8_t *q, const float *d, const int16_t *bs, const uint8_t *bad);
 
 int launch_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c, int64_t M,
-                bool acc, const int8_t *q, const float *d, const int16_t *bs, const int32_t *flags) {
+                bool acc, const int8_t *q, const float *d, const int16_t *bs, const uint8_t *bad) {
     if (N == 0 || M == 0) return TRHIP_OK;
     switch (w->dtype) {
-    case kQ4: return run_valu<kQ4>(ctx, w, row0, N, x, c, M, acc, q, d, bs, flags);
-    case kQ4K: return run_valu<kQ4K>(ctx, w, row0, N, x, c, M, acc, q, d, bs, flags);
-    case kQ6K: return run_valu<kQ6K>(ctx, w, row0, N, x, c, M, acc, q, d, bs, flags);
+    case kQ4: return run_valu<kQ4>(ctx, w, row0, N, x, c, M, acc, q, d, bs, bad);
+    case kQ4K: return run_valu<kQ4K>(ctx, w, row0, N, x, c, M, acc, q, d, bs, bad);
+    case kQ6K: return run_valu<kQ6K>(ctx, w, row0, N, x, c, M, acc, q, d, bs, bad);
     }
     return fail(ctx, TRHIP_ERR_UNSUPPORTED, "actq: dtype must be q4, q4_k or q6_k");
 }

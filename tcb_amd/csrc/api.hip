@@ -32,6 +32,11 @@ int launch_check(trhip_ctx *ctx, const char *what) {
 void *workspace(trhip_ctx *ctx, size_t bytes, int *status) {
     *status = TRHIP_OK;
     if (bytes <= ctx->ws_bytes) return ctx->ws;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(ctx->stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
+        *status = fail(ctx, TRHIP_ERR_INVALID, "workspace must be sized by an eager call before graph capture");
+        return nullptr;
+    }
     // Growing: earlier work on the stream may still read the old buffer.
     hipError_t e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) { *status = hip_fail(ctx, e, "workspace sync"); return nullptr; }
@@ -43,6 +48,18 @@ void *workspace(trhip_ctx *ctx, size_t bytes, int *status) {
     if (e != hipSuccess) { ctx->ws = nullptr; *status = hip_fail(ctx, e, "workspace alloc"); return nullptr; }
     ctx->ws_bytes = want;
     return ctx->ws;
+}
+
+__global__ void zero_f32_kernel(float *__restrict__ p, int64_t n) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0.0f;
+}
+
+// Zero n floats with a kernel (safe inside graph capture, unlike a memset node).
+int zero_f32(trhip_ctx *ctx, float *p, int64_t n) {
+    if (n <= 0) return TRHIP_OK;
+    hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream, p, n);
+    return launch_check(ctx, "zero");
 }
 
 }  // namespace trhip
@@ -134,6 +151,8 @@ int trhip_destroy(trhip_ctx *ctx) {
     DevGuard g(ctx);
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->fast.partials) (void)hipFree(ctx->fast.partials);
+    if (ctx->fast.counters) (void)hipFree(ctx->fast.counters);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return TRHIP_OK;
@@ -217,6 +236,40 @@ int trhip_event_elapsed_ms(void *a, void *b, float *ms) {
 int trhip_event_destroy(void *ev) {
     if (!ev) return TRHIP_ERR_INVALID;
     return hipEventDestroy((hipEvent_t)ev) == hipSuccess ? TRHIP_OK : TRHIP_ERR_HIP;
+}
+
+int trhip_graph_begin(trhip_ctx *ctx) {
+    if (!ctx) return TRHIP_ERR_INVALID;
+    DevGuard g(ctx);
+    hipError_t e = hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal);
+    return e == hipSuccess ? TRHIP_OK : hip_fail(ctx, e, "graph begin");
+}
+
+int trhip_graph_end(trhip_ctx *ctx, void **exec) {
+    if (!ctx || !exec) return TRHIP_ERR_INVALID;
+    DevGuard g(ctx);
+    *exec = nullptr;
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
+    if (e != hipSuccess) return hip_fail(ctx, e, "graph end");
+    hipGraphExec_t ge = nullptr;
+    e = hipGraphInstantiate(&ge, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) return hip_fail(ctx, e, "graph instantiate");
+    *exec = (void *)ge;
+    return TRHIP_OK;
+}
+
+int trhip_graph_launch(trhip_ctx *ctx, void *exec) {
+    if (!ctx || !exec) return TRHIP_ERR_INVALID;
+    DevGuard g(ctx);
+    hipError_t e = hipGraphLaunch((hipGraphExec_t)exec, ctx->stream);
+    return e == hipSuccess ? TRHIP_OK : hip_fail(ctx, e, "graph launch");
+}
+
+int trhip_graph_destroy(void *exec) {
+    if (!exec) return TRHIP_ERR_INVALID;
+    return hipGraphExecDestroy((hipGraphExec_t)exec) == hipSuccess ? TRHIP_OK : TRHIP_ERR_HIP;
 }
 
 int trhip_check_quant_scales(int dtype, const void *raw, size_t raw_bytes, int64_t *bad_block) {
@@ -335,7 +388,7 @@ int trhip_gemm_q(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N,
     DevGuard g(ctx);
     if (K == 0) {  // empty sum (gpu/backend_quant.go:51-56)
         if (accumulate) return TRHIP_OK;
-        return trhip_memset_async(ctx, c, 0, (size_t)(M * N) * sizeof(float));
+        return zero_f32(ctx, c, M * N);
     }
     if (!x || !c) return fail(ctx, TRHIP_ERR_INVALID, "gemm_q: null x or c");
     if (M == 1) {
@@ -360,11 +413,9 @@ int trhip_quantize_q8(trhip_ctx *ctx, const float *x, int64_t M, int64_t K, int 
     if (!x || !q || !d || !bs || reinterpret_cast<uintptr_t>(x) % 16 != 0) return fail(ctx, TRHIP_ERR_INVALID, "quantize_q8: pointers");
     DevGuard g(ctx);
     int st = TRHIP_OK;
-    int32_t *flags = static_cast<int32_t *>(workspace(ctx, (size_t)M * sizeof(int32_t), &st));
-    if (!flags) return st;
-    hipError_t e = hipMemsetAsync(flags, 0, (size_t)M * sizeof(int32_t), ctx->stream);
-    if (e != hipSuccess) return hip_fail(ctx, e, "quantize_q8: flags");
-    return launch_quantize_q8(ctx, x, M, K, blk, q, d, bs, flags);
+    uint8_t *bad = static_cast<uint8_t *>(workspace(ctx, (size_t)(M * (K / blk)), &st));
+    if (!bad) return st;
+    return launch_quantize_q8(ctx, x, M, K, blk, q, d, bs, bad);
 }
 
 int trhip_gemm_q_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
@@ -377,7 +428,7 @@ int trhip_gemm_q_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64
     DevGuard g(ctx);
     if (K == 0) {
         if (accumulate) return TRHIP_OK;
-        return trhip_memset_async(ctx, c, 0, (size_t)(M * N) * sizeof(float));
+        return zero_f32(ctx, c, M * N);
     }
     if (!x || !c) return fail(ctx, TRHIP_ERR_INVALID, "gemm_q_actq: null x or c");
     int blk = block_elems(w->dtype);
@@ -386,7 +437,7 @@ int trhip_gemm_q_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64
     size_t o_d = align_up(o_q + (size_t)(M * K), 256);
     size_t o_bs = align_up(o_d + (size_t)(M * nb) * sizeof(float), 256);
     size_t o_fl = align_up(o_bs + (size_t)(M * (K / 16)) * sizeof(int16_t), 256);
-    size_t o_x = align_up(o_fl + (size_t)M * sizeof(int32_t), 256);
+    size_t o_x = align_up(o_fl + (size_t)(M * nb), 256);
     bool copy_x = reinterpret_cast<uintptr_t>(x) % 16 != 0;
     size_t total = o_x + (copy_x ? (size_t)(M * K) * sizeof(float) : 0);
     int st = TRHIP_OK;
@@ -395,7 +446,7 @@ int trhip_gemm_q_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64
     int8_t *q = reinterpret_cast<int8_t *>(ws + o_q);
     float *d = reinterpret_cast<float *>(ws + o_d);
     int16_t *bs = reinterpret_cast<int16_t *>(ws + o_bs);
-    int32_t *flags = reinterpret_cast<int32_t *>(ws + o_fl);
+    uint8_t *bad = ws + o_fl;  // one flag byte per activation block (NaN/Inf present)
     const float *xa = x;
     if (copy_x) {
         float *tmp = reinterpret_cast<float *>(ws + o_x);
@@ -403,10 +454,8 @@ int trhip_gemm_q_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64
         if (e != hipSuccess) return hip_fail(ctx, e, "gemm_q_actq: align x");
         xa = tmp;
     }
-    hipError_t e = hipMemsetAsync(flags, 0, (size_t)M * sizeof(int32_t), ctx->stream);
-    if (e != hipSuccess) return hip_fail(ctx, e, "gemm_q_actq: flags");
-    if ((st = launch_quantize_q8(ctx, xa, M, K, blk, q, d, bs, flags)) != TRHIP_OK) return st;
-    return launch_actq(ctx, w, row0, N, xa, c, M, accumulate != 0, q, d, bs, flags);
+    if ((st = launch_quantize_q8(ctx, xa, M, K, blk, q, d, bs, bad)) != TRHIP_OK) return st;
+    return launch_actq(ctx, w, row0, N, xa, c, M, accumulate != 0, q, d, bs, bad);
 }
 
 int trhip_open_q(trhip_ctx *ctx, const trhip_wstore *w, int64_t elem_off, int64_t n, float *out) {

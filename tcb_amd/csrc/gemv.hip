@@ -10,25 +10,47 @@
 // both partners hold the same bits), the rest is in-lane. Dequantized values are produced exactly as in
 // tensor/quant.go: exact products, one rounding where the reference rounds (fmaf of exact operands).
 //
-// Bandwidth: every weight byte is read once, with 128-bit loads where the plane layout allows; x is
-// read through the cache (it is shared by all rows).
+// Latency hiding: x is staged once per workgroup in LDS; each lane keeps a ring of DEPTH blocks of
+// weight bytes in registers and issues the loads for block b+DEPTH before it computes block b, so every
+// wave has DEPTH blocks of HBM reads in flight. Every weight byte is read exactly once.
 #include "trhip_internal.hpp"
+
+#include <cstdlib>
 
 namespace trhip {
 namespace {
 
-constexpr int kRowsPerWG = 16;  // 64 threads: 16 rows x 4 lanes
+// Stage n float4 of x into LDS with `threads` threads: all loads of a batch are issued before any
+// store so the L2 round trips overlap.
+template <int THREADS>
+__device__ __forceinline__ void stage_x(float4 *xs, const float4 *__restrict__ x4, int64_t n) {
+    constexpr int U = 8;
+    for (int64_t i0 = 0; i0 < n; i0 += (int64_t)U * THREADS) {
+        float4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {  // clamped, unconditional loads keep v[] in registers
+            int64_t i = i0 + (int64_t)u * THREADS + threadIdx.x;
+            v[u] = x4[i < n ? i : n - 1];
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            int64_t i = i0 + (int64_t)u * THREADS + threadIdx.x;
+            if (i < n) xs[i] = v[u];
+        }
+    }
+}
 
 __device__ __forceinline__ void fma4(float *acc, uint32_t codes, float s, float negm, float4 xv) {
+    codes = opaque(codes);
     acc[0] = fmaf(fmaf(s, ubyte_f(codes, 0), negm), xv.x, acc[0]);
     acc[1] = fmaf(fmaf(s, ubyte_f(codes, 1), negm), xv.y, acc[1]);
     acc[2] = fmaf(fmaf(s, ubyte_f(codes, 2), negm), xv.z, acc[2]);
     acc[3] = fmaf(fmaf(s, ubyte_f(codes, 3), negm), xv.w, acc[3]);
 }
 
-// One 32-element group for this lane: 8 codes (two dwords), value = fmaf(s, code, negm).
+// One 32-element group for this lane: 8 codes (two dwords), value = fmaf(s, code, negm); x from LDS.
 __device__ __forceinline__ void group8(float *acc, uint32_t c0, uint32_t c1, float s, float negm,
-                                       const float4 *__restrict__ xg) {
+                                       const float4 *xg) {
     float4 xa = xg[0], xb = xg[1];
     fma4(acc, c0, s, negm, xa);
     fma4(acc + 4, c1, s, negm, xb);
@@ -45,117 +67,205 @@ __device__ __forceinline__ float sdot32_tree(float *acc) {
     return (s0 + s2) + (s1 + s3);
 }
 
-template <int DT, bool ACC>
-__global__ __launch_bounds__(64) void gemv_exact_kernel(const Planes p, const float *__restrict__ x,
-                                                        float *__restrict__ c, int64_t N, int64_t row0) {
-    const int t = threadIdx.x & 3;
-    const int64_t r = (int64_t)blockIdx.x * kRowsPerWG + (threadIdx.x >> 2);
-    if (r >= N) return;  // the whole quad leaves together
-    const int64_t row = row0 + r;
-    const int64_t nb = p.nb;
-    float acc[8];
-#pragma unroll
-    for (int l = 0; l < 8; l++) acc[l] = 0.0f;
-    // element 32G + 8t -> float4 index 8G + 2t
-    const float4 *__restrict__ xv = reinterpret_cast<const float4 *>(x) + 2 * t;
+// Per-dtype block access. Data holds one block's bytes for one lane; load() fetches block b of the
+// lane's row; compute() advances the lane's eight chains over that block. xb points at the LDS copy
+// of x, at float4 index 2t of the block's first element.
+template <int DT>
+struct Blk;
 
-    if (DT == kQ8) {
-        const uint2 *__restrict__ qp = reinterpret_cast<const uint2 *>(p.qs + row * nb * 32) + t;
-        const uint16_t *__restrict__ dp = p.d + row * nb;
-        for (int64_t b = 0; b < nb; b++) {
-            uint2 q = qp[4 * b];
-            float d = f16_to_f32(dp[b]);
-            // code = u - 128 with u = byte ^ 0x80; value (u-128)*d is exact, so fmaf(d, u, -128d) is too
-            group8(acc, q.x ^ 0x80808080u, q.y ^ 0x80808080u, d, -128.0f * d, xv + 8 * b);
-        }
-    } else if (DT == kQ4) {
-        const uint2 *__restrict__ qp = reinterpret_cast<const uint2 *>(p.qs + row * nb * 16) + (t & 1);
-        const uint16_t *__restrict__ dp = p.d + row * nb;
-        const int sh = (t & 2) ? 4 : 0;  // lanes 2,3 take the high nibbles (elements 16..31)
-        for (int64_t b = 0; b < nb; b++) {
-            uint2 q = qp[2 * b];
-            float d = f16_to_f32(dp[b]);
-            group8(acc, (q.x >> sh) & 0x0F0F0F0Fu, (q.y >> sh) & 0x0F0F0F0Fu, d, -8.0f * d, xv + 8 * b);
-        }
-    } else if (DT == kQ4K) {
-        const uint4 *__restrict__ hp = reinterpret_cast<const uint4 *>(p.aux + row * nb * 16);
-        const uint4 *__restrict__ qp = reinterpret_cast<const uint4 *>(p.qs + row * nb * 128 + 32 * t);
-        for (int64_t b = 0; b < nb; b++) {
-            uint4 h = hp[b];
-            uint4 qa = qp[8 * b], qb = qp[8 * b + 1];
-            float d = f16_to_f32((uint16_t)(h.x & 0xFFFF)), dmin = f16_to_f32((uint16_t)(h.x >> 16));
-            float d16 = d * 0.0625f;
-            uint32_t sc_lo, sc_hi, m_lo, m_hi;
-            q4k_scales(h.y, h.z, h.w, sc_lo, sc_hi, m_lo, m_hi);
-            const float4 *xb = xv + 64 * b;
-            uint32_t w[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+template <>
+struct Blk<kQ8> {
+    static constexpr int DEPTH = 16;
+    struct Data { uint2 q; uint32_t d; };
+    const uint2 *qp;
+    const uint16_t *dp;
+    __device__ Blk(const Planes &p, int64_t row, int t)
+        : qp(reinterpret_cast<const uint2 *>(p.qs + row * p.nb * 32) + t), dp(p.d + row * p.nb) {}
+    __device__ __forceinline__ void load(Data &v, int64_t b) const { v.q = qp[4 * b]; v.d = dp[b]; }
+    __device__ __forceinline__ void compute(float *acc, const Data &v, const float4 *xb, int t) const {
+        float d = f16_to_f32((uint16_t)v.d);
+        // code = u - 128 with u = byte ^ 0x80; (u-128)*d is exact, so fmaf(d, u, -128d) is too
+        group8(acc, v.q.x ^ 0x80808080u, v.q.y ^ 0x80808080u, d, -128.0f * d, xb);
+    }
+    static constexpr int XSTEP = 8;  // float4s of x per block
+};
+
+template <>
+struct Blk<kQ4> {
+    static constexpr int DEPTH = 16;
+    struct Data { uint2 q; uint32_t d; };
+    const uint2 *qp;
+    const uint16_t *dp;
+    int sh;
+    __device__ Blk(const Planes &p, int64_t row, int t)
+        : qp(reinterpret_cast<const uint2 *>(p.qs + row * p.nb * 16) + (t & 1)), dp(p.d + row * p.nb),
+          sh((t & 2) ? 4 : 0) {}  // lanes 2,3 take the high nibbles (elements 16..31)
+    __device__ __forceinline__ void load(Data &v, int64_t b) const { v.q = qp[2 * b]; v.d = dp[b]; }
+    __device__ __forceinline__ void compute(float *acc, const Data &v, const float4 *xb, int t) const {
+        float d = f16_to_f32((uint16_t)v.d);
+        group8(acc, (v.q.x >> sh) & 0x0F0F0F0Fu, (v.q.y >> sh) & 0x0F0F0F0Fu, d, -8.0f * d, xb);
+    }
+    static constexpr int XSTEP = 8;
+};
+
+template <>
+struct Blk<kQ4K> {
+    static constexpr int DEPTH = 6;
+    struct Data { uint4 h; uint2 q[4]; };
+    const uint4 *hp;
+    const uint2 *qp;  // lane t's piece of group g sits at byte 64(t>>1) + 16g + 8(t&1) of the block
+    __device__ Blk(const Planes &p, int64_t row, int t)
+        : hp(reinterpret_cast<const uint4 *>(p.aux + row * p.nb * 16)),
+          qp(reinterpret_cast<const uint2 *>(p.qs + row * p.nb * 128) + 8 * (t >> 1) + (t & 1)) {}
+    __device__ __forceinline__ void load(Data &v, int64_t b) const {
+        v.h = hp[b];
 #pragma unroll
-            for (int g = 0; g < 4; g++) {
-                uint32_t scw = g < 2 ? sc_lo : sc_hi, mw = g < 2 ? m_lo : m_hi;
-                int k0 = (2 * g) & 3, k1 = (2 * g + 1) & 3;
-                float s0 = d * ubyte_f(scw, k0), n0 = -(dmin * ubyte_f(mw, k0));
-                float s1 = d16 * ubyte_f(scw, k1), n1 = -(dmin * ubyte_f(mw, k1));
-                // sub-block 2g: low nibbles; sub-block 2g+1: high nibbles used as 16*code (scale d/16)
-                group8(acc, w[2 * g] & 0x0F0F0F0Fu, w[2 * g + 1] & 0x0F0F0F0Fu, s0, n0, xb + 8 * (2 * g));
-                group8(acc, w[2 * g] & 0xF0F0F0F0u, w[2 * g + 1] & 0xF0F0F0F0u, s1, n1, xb + 8 * (2 * g + 1));
-            }
+        for (int g = 0; g < 4; g++) v.q[g] = qp[16 * b + 2 * g];
+    }
+    __device__ __forceinline__ void compute(float *acc, const Data &v, const float4 *xb, int t) const {
+        float d = f16_to_f32((uint16_t)(v.h.x & 0xFFFF)), dmin = f16_to_f32((uint16_t)(v.h.x >> 16));
+        float d16 = d * 0.0625f;
+        uint32_t sc_lo, sc_hi, m_lo, m_hi;
+        q4k_scales(v.h.y, v.h.z, v.h.w, sc_lo, sc_hi, m_lo, m_hi);
+        uint32_t w[8] = {v.q[0].x, v.q[0].y, v.q[1].x, v.q[1].y, v.q[2].x, v.q[2].y, v.q[3].x, v.q[3].y};
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            uint32_t scw = g < 2 ? sc_lo : sc_hi, mw = g < 2 ? m_lo : m_hi;
+            int k0 = (2 * g) & 3, k1 = (2 * g + 1) & 3;
+            float s0 = d * ubyte_f(scw, k0), n0 = -(dmin * ubyte_f(mw, k0));
+            float s1 = d16 * ubyte_f(scw, k1), n1 = -(dmin * ubyte_f(mw, k1));
+            // sub-block 2g: low nibbles; sub-block 2g+1: high nibbles used as 16*code (scale d/16)
+            group8(acc, w[2 * g] & 0x0F0F0F0Fu, w[2 * g + 1] & 0x0F0F0F0Fu, s0, n0, xb + 8 * (2 * g));
+            group8(acc, w[2 * g] & 0xF0F0F0F0u, w[2 * g + 1] & 0xF0F0F0F0u, s1, n1, xb + 8 * (2 * g + 1));
         }
-    } else {  // q6_k
-        const uint4 *__restrict__ lp = reinterpret_cast<const uint4 *>(p.qs + row * nb * 128 + 32 * t);
-        const uint4 *__restrict__ hp = reinterpret_cast<const uint4 *>(p.aux + row * nb * 64 + 16 * t);
-        const uint4 *__restrict__ sp = reinterpret_cast<const uint4 *>(p.sc + row * nb * 16);
-        const uint16_t *__restrict__ dp = p.d + row * nb;
+    }
+    static constexpr int XSTEP = 64;
+};
+
+template <>
+struct Blk<kQ6K> {
+    static constexpr int DEPTH = 5;
+    struct Data { uint4 la, lb, hh, sv; uint32_t d; };
+    const uint4 *lp, *hp, *sp;
+    const uint16_t *dp;
+    __device__ Blk(const Planes &p, int64_t row, int t)
+        : lp(reinterpret_cast<const uint4 *>(p.qs + row * p.nb * 128 + 32 * t)),
+          hp(reinterpret_cast<const uint4 *>(p.aux + row * p.nb * 64 + 16 * t)),
+          sp(reinterpret_cast<const uint4 *>(p.sc + row * p.nb * 16)), dp(p.d + row * p.nb) {}
+    __device__ __forceinline__ void load(Data &v, int64_t b) const {
+        v.la = lp[8 * b];
+        v.lb = lp[8 * b + 1];
+        v.hh = hp[4 * b];
+        v.sv = sp[b];
+        v.d = dp[b];
+    }
+    __device__ __forceinline__ void compute(float *acc, const Data &v, const float4 *xb, int t) const {
+        float d = f16_to_f32((uint16_t)v.d);
+        uint32_t scw[4] = {v.sv.x, v.sv.y, v.sv.z, v.sv.w};
         const int th = t >> 1;
-        for (int64_t b = 0; b < nb; b++) {
-            uint4 la = lp[8 * b], lb = lp[8 * b + 1], hh = hp[4 * b], sv = sp[b];
-            float d = f16_to_f32(dp[b]);
-            uint32_t scw[4] = {sv.x, sv.y, sv.z, sv.w};
-            const float4 *xb = xv + 64 * b;
 #pragma unroll
-            for (int n = 0; n < 2; n++) {
-                uint32_t A0 = n ? lb.x : la.x, A1 = n ? lb.y : la.y;  // ql[64n + 8t + l]
-                uint32_t B0 = n ? lb.z : la.z, B1 = n ? lb.w : la.w;  // ql[64n + 32 + 8t + l]
-                uint32_t H0 = n ? hh.z : hh.x, H1 = n ? hh.w : hh.y;  // qh[32n + 8t + l]
+        for (int n = 0; n < 2; n++) {
+            uint32_t A0 = n ? v.lb.x : v.la.x, A1 = n ? v.lb.y : v.la.y;  // ql[64n + 8t + l]
+            uint32_t B0 = n ? v.lb.z : v.la.z, B1 = n ? v.lb.w : v.la.w;  // ql[64n + 32 + 8t + l]
+            uint32_t H0 = n ? v.hh.z : v.hh.x, H1 = n ? v.hh.w : v.hh.y;  // qh[32n + 8t + l]
 #pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    uint32_t c0, c1;
-                    if (k == 0) {
-                        c0 = (A0 & 0x0F0F0F0Fu) | ((H0 << 4) & 0x30303030u);
-                        c1 = (A1 & 0x0F0F0F0Fu) | ((H1 << 4) & 0x30303030u);
-                    } else if (k == 1) {
-                        c0 = (B0 & 0x0F0F0F0Fu) | ((H0 << 2) & 0x30303030u);
-                        c1 = (B1 & 0x0F0F0F0Fu) | ((H1 << 2) & 0x30303030u);
-                    } else if (k == 2) {
-                        c0 = ((A0 >> 4) & 0x0F0F0F0Fu) | (H0 & 0x30303030u);
-                        c1 = ((A1 >> 4) & 0x0F0F0F0Fu) | (H1 & 0x30303030u);
-                    } else {
-                        c0 = ((B0 >> 4) & 0x0F0F0F0Fu) | ((H0 >> 2) & 0x30303030u);
-                        c1 = ((B1 >> 4) & 0x0F0F0F0Fu) | ((H1 >> 2) & 0x30303030u);
-                    }
-                    int si = 8 * n + 2 * k + th;  // 16-element sub-block of these 8 elements
-                    int8_t scv = (int8_t)((scw[si >> 2] >> (8 * (si & 3))) & 0xFF);
-                    float ds = d * (float)scv;  // exact (11 x 8 bits)
-                    // value fl(ds*(code-32)) == fmaf(ds, code, -32*ds): same real number, one rounding
-                    group8(acc, c0, c1, ds, -32.0f * ds, xb + 8 * (4 * n + k));
+            for (int k = 0; k < 4; k++) {
+                uint32_t c0, c1;
+                if (k == 0) {
+                    c0 = (A0 & 0x0F0F0F0Fu) | ((H0 << 4) & 0x30303030u);
+                    c1 = (A1 & 0x0F0F0F0Fu) | ((H1 << 4) & 0x30303030u);
+                } else if (k == 1) {
+                    c0 = (B0 & 0x0F0F0F0Fu) | ((H0 << 2) & 0x30303030u);
+                    c1 = (B1 & 0x0F0F0F0Fu) | ((H1 << 2) & 0x30303030u);
+                } else if (k == 2) {
+                    c0 = ((A0 >> 4) & 0x0F0F0F0Fu) | (H0 & 0x30303030u);
+                    c1 = ((A1 >> 4) & 0x0F0F0F0Fu) | (H1 & 0x30303030u);
+                } else {
+                    c0 = ((B0 >> 4) & 0x0F0F0F0Fu) | ((H0 >> 2) & 0x30303030u);
+                    c1 = ((B1 >> 4) & 0x0F0F0F0Fu) | ((H1 >> 2) & 0x30303030u);
                 }
+                int si = 8 * n + 2 * k + th;  // 16-element sub-block of these 8 elements
+                int8_t scv = (int8_t)((scw[si >> 2] >> (8 * (si & 3))) & 0xFF);
+                float ds = d * (float)scv;  // exact (11 x 8 bits)
+                // value fl(ds*(code-32)) == fmaf(ds, code, -32*ds): same real number, one rounding
+                group8(acc, c0, c1, ds, -32.0f * ds, xb + 8 * (4 * n + k));
             }
         }
     }
+    static constexpr int XSTEP = 64;
+};
+
+template <int DT, bool ACC, int THREADS>
+__global__ __launch_bounds__(THREADS) void gemv_exact_kernel(const Planes p, const float *__restrict__ x,
+                                                             float *__restrict__ c, int64_t N, int64_t row0, int64_t K) {
+    extern __shared__ float4 xs[];  // K / 4 float4: the whole activation vector
+    const int t = threadIdx.x & 3;
+    const int64_t r = (int64_t)blockIdx.x * (THREADS / 4) + (threadIdx.x >> 2);
+    const bool live = r < N;
+    const int64_t row = row0 + (live ? r : 0);
+    const int64_t nb = p.nb;
+    using B = Blk<DT>;
+    constexpr int D = B::DEPTH;
+    B blk(p, row, t);
+    typename B::Data ring[D];
+    // weights first (they come from HBM), then x into LDS
+#pragma unroll
+    for (int s = 0; s < D; s++) blk.load(ring[s], s < nb ? s : nb - 1);
+    stage_x<THREADS>(xs, reinterpret_cast<const float4 *>(x), K / 4);
+    __syncthreads();
+
+    float acc[8];
+#pragma unroll
+    for (int l = 0; l < 8; l++) acc[l] = 0.0f;
+    const float4 *xl = xs + 2 * t;
+    // Loads are unconditional (clamped to the last block, re-reading it at the tail) so the ring stays
+    // in registers with static indices; only the compute is guarded, by a wave-uniform test.
+    for (int64_t b0 = 0; b0 < nb; b0 += D) {
+#pragma unroll
+        for (int s = 0; s < D; s++) {
+            const int64_t b = b0 + s;
+            typename B::Data cur = ring[s];
+            blk.load(ring[s], (b + D < nb) ? b + D : nb - 1);
+            if (b < nb) blk.compute(acc, cur, xl + B::XSTEP * b, t);
+        }
+    }
     float res = sdot32_tree(acc);
-    if (t == 0) {
+    if (live && t == 0) {
         if (ACC) c[r] = c[r] + res;
         else c[r] = res;
     }
 }
 
+template <int DT, int THREADS>
+void launch_exact_t(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
+                    bool acc, size_t lds) {
+    dim3 grid((unsigned)((N + THREADS / 4 - 1) / (THREADS / 4))), block(THREADS);
+    if (acc)
+        hipLaunchKernelGGL((gemv_exact_kernel<DT, true, THREADS>), grid, block, lds, ctx->stream, w->planes(), x, c, N, row0, w->K);
+    else
+        hipLaunchKernelGGL((gemv_exact_kernel<DT, false, THREADS>), grid, block, lds, ctx->stream, w->planes(), x, c, N, row0, w->K);
+}
+
+// Rows per workgroup: TRHIP_GEMV_ROWS (16, 32 or 64) overrides the default of 16.
+int gemv_rows_per_wg() {
+    static int v = [] {
+        const char *e = getenv("TRHIP_GEMV_ROWS");
+        int r = e ? atoi(e) : 16;
+        return (r == 32 || r == 64) ? r : 16;
+    }();
+    return v;
+}
+
 template <int DT>
 int launch_exact(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                  bool acc) {
-    dim3 grid((unsigned)((N + kRowsPerWG - 1) / kRowsPerWG)), block(64);
-    if (acc)
-        hipLaunchKernelGGL((gemv_exact_kernel<DT, true>), grid, block, 0, ctx->stream, w->planes(), x, c, N, row0);
-    else
-        hipLaunchKernelGGL((gemv_exact_kernel<DT, false>), grid, block, 0, ctx->stream, w->planes(), x, c, N, row0);
+    size_t lds = (size_t)w->K * sizeof(float);
+    if (lds > 160 * 1024) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv: K too large for the LDS copy of x");
+    switch (gemv_rows_per_wg()) {
+    case 64: launch_exact_t<DT, 256>(ctx, w, row0, N, x, c, acc, lds); break;
+    case 32: launch_exact_t<DT, 128>(ctx, w, row0, N, x, c, acc, lds); break;
+    default: launch_exact_t<DT, 64>(ctx, w, row0, N, x, c, acc, lds); break;
+    }
     return launch_check(ctx, "gemv_exact");
 }
 

@@ -1,12 +1,253 @@
-// gemv_fast.hip -- decode GEMV in the factored (tolerance-bound) order. Placeholder: routes to the exact
-// kernels until the factored kernels land.
+// gemv_fast.hip -- decode GEMV (M == 1) in factored order: within the north-star tolerance
+// (|a-b|/(1+|b|) <= 1e-5, 1e-4 for K-quants), not bit-identical to TR's CPU path.
+//
+// Per 32-element sub-block j (16 for q6_k) with value y = s_j*q - m_j (tensor/quant.go:139-205):
+//   sum_e y_e x_e = s_j * (sum_e q_e x_e) - m_j * (sum_e x_e)
+// so the inner loop is one convert and one fused multiply-add per weight. The x sums are the same for
+// every row and are computed once per workgroup into LDS.
+//
+// Mapping: a wave is 64 rows (lane = row), all lanes on the same block, so x is wave-uniform and is
+// read with scalar loads. A workgroup is 64 rows x WAVES waves; wave w takes BPW consecutive blocks; a
+// grid column (blockIdx.y) takes WAVES*BPW blocks. Partial sums are combined in a fixed order: the
+// waves of a workgroup through LDS, the workgroups of a row tile through a partials buffer summed by
+// whichever workgroup arrives last (integer arrival counter, reset by that workgroup). No float atomics,
+// so the result depends only on the shape (the reference forbids atomic accumulation on this path,
+// gpu/kernel_quant_gemv.go:14-16).
 #include "trhip_internal.hpp"
 
+#include <cstdlib>
+
 namespace trhip {
+namespace {
+
+constexpr int kWaves = 4;
+
+template <int k>
+__device__ __forceinline__ float ub(uint32_t v) { return ubyte_f(v, k); }
+
+// x sums for this workgroup's blocks: sx[i] = sum of x over 16-element group i (relative to k0).
+__device__ __forceinline__ void x_sums16(float *sx, const float *__restrict__ x, int64_t k0, int ngroups) {
+    for (int i = threadIdx.x; i < ngroups; i += blockDim.x) {
+        const float4 *p = reinterpret_cast<const float4 *>(x + k0 + 16 * (int64_t)i);
+        float4 a = p[0], b = p[1], c = p[2], d = p[3];
+        sx[i] = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w)) + ((c.x + c.y) + (c.z + c.w)) +
+                ((d.x + d.y) + (d.z + d.w));
+    }
+}
+
+// Fixed-order reduction of the WAVES partials per row inside the workgroup, then across grid columns.
+template <bool ACC>
+__device__ __forceinline__ void finish(float part, float *lds_part, float *__restrict__ c, float *__restrict__ partials,
+                                       int *__restrict__ counters, int64_t N, int64_t r, int ncol) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    lds_part[w * 64 + lane] = part;
+    __syncthreads();
+    if (w != 0) return;
+    float s = lds_part[lane];
+#pragma unroll
+    for (int i = 1; i < kWaves; i++) s = s + lds_part[i * 64 + lane];
+    if (ncol == 1) {
+        if (r < N) c[r] = ACC ? c[r] + s : s;
+        return;
+    }
+    if (r < N) partials[(int64_t)blockIdx.y * N + r] = s;
+    __shared__ int last;
+    __threadfence();  // our partials are visible device-wide before we count ourselves in
+    // one arrival per workgroup; the last one to arrive sums every column in column order
+    if (lane == 0) {
+        int old = __hip_atomic_fetch_add(counters + blockIdx.x, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        last = (old == ncol - 1);
+        if (last) __hip_atomic_store(counters + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_wave_barrier();
+    __threadfence();
+    if (!last || r >= N) return;
+    float t = __hip_atomic_load(partials + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int i = 1; i < ncol; i++) t = t + __hip_atomic_load(partials + (int64_t)i * N + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    c[r] = ACC ? c[r] + t : t;
+}
+
+// ---------------------------------------------------------------- q4_k
+// Nibble pairs to floats: a byte holding 0..15, read as an OCP FP8 E4M3 value, is exactly q * 2^-9
+// (subnormals below 8, the first binade above), so one v_cvt_pk_f32_fp8 converts two codes. The 2^9
+// goes into the sub-block scale, which stays exact (a power of two).
+__device__ __forceinline__ void fma_nib4(float &p, uint32_t nib4, float4 xv) {
+    auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)nib4, false);  // bytes 0, 1
+    auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)nib4, true);   // bytes 2, 3
+    p = fmaf(lo[0], xv.x, p);
+    p = fmaf(lo[1], xv.y, p);
+    p = fmaf(hi[0], xv.z, p);
+    p = fmaf(hi[1], xv.w, p);
+}
+
+// Eight lanes per row; lane (g, h) = (lane8 >> 1, lane8 & 1) owns the 16 qs bytes 32g + 16h .. +16 of
+// every block: low nibbles are elements 16h..16h+15 of sub-block 2g, high nibbles the same elements of
+// sub-block 2g+1. A workgroup is 16 rows x 2 halves of K: wave w takes rows 8*(w>>1)..+8 and blocks of
+// half w&1. The halves meet in LDS (half 0 + half 1), then the 8 lanes of a row add with a fixed
+// xor-butterfly. x lives in LDS with a 16-byte pad per 256 bytes (the 8 slices a wave reads per step fall
+// in distinct banks), its 16-element sums next to it. Weights and x are both read one step ahead.
+template <bool ACC, int D>
+__global__ __launch_bounds__(256) void gemv_fast_q4k(const Planes p, const float *__restrict__ x,
+                                                     float *__restrict__ c, int64_t N, int64_t row0, int64_t K) {
+    extern __shared__ float4 lds4[];
+    __shared__ float half_part[128];
+    const int nx4 = (int)(K / 4);
+    float4 *xs = lds4;                                             // padded: nx4 + nx4/16 float4
+    float *sx = reinterpret_cast<float *>(lds4 + nx4 + nx4 / 16);  // K/16 floats
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane8 = lane & 7, g = lane8 >> 1, hsel = lane8 & 1;
+    const int64_t r = (int64_t)blockIdx.x * 16 + 8 * (w >> 1) + (lane >> 3);
+    const int64_t row = row0 + (r < N ? r : N - 1);
+    const int nb = (int)p.nb;
+    const int nh = (nb + 1) / 2;
+    const int b0 = (w & 1) ? nh : 0, b1 = (w & 1) ? nb : nh;
+    const uint4 *hp = reinterpret_cast<const uint4 *>(p.aux) + row * nb;
+    const uint4 *qp = reinterpret_cast<const uint4 *>(p.qs) + row * nb * 8 + 4 * hsel + g;
+    uint4 H[D], Q[D];
+#pragma unroll
+    for (int s = 0; s < D; s++) {  // weights first: they come from HBM
+        int b = b0 + s < b1 ? b0 + s : (b1 > b0 ? b1 - 1 : 0);
+        H[s] = hp[b];
+        Q[s] = qp[8 * b];
+    }
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+    for (int i = threadIdx.x; i < (int)(K / 16); i += 256) {
+        float4 a = x4[4 * i], b = x4[4 * i + 1], cc = x4[4 * i + 2], dd = x4[4 * i + 3];
+        float4 *o = xs + 4 * i + (i >> 2);  // padded index of 4i: 4i + (4i >> 4)
+        o[0] = a;
+        o[1] = b;
+        o[2] = cc;
+        o[3] = dd;
+        sx[i] = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w)) + ((cc.x + cc.y) + (cc.z + cc.w)) +
+                ((dd.x + dd.y) + (dd.z + dd.w));
+    }
+    __syncthreads();
+    const int k0 = (2 * g) & 3, k1 = (2 * g + 1) & 3;
+    // x of elements 256b + 64g + 16h + 4c (+32 for the high nibbles): float4 64b + 16g + 4h + c, padded
+    // by (64b + 16g + 4h + c) >> 4 = 4b + g
+    const float4 *xg = xs + 17 * g + 4 * hsel;
+    const float *sxg = sx + 4 * g + hsel;
+    float4 XL[4], XH[4];
+    {
+        const float4 *xb = xg + 68 * (b0 < b1 ? b0 : 0);
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++) {
+            XL[cc] = xb[cc];
+            XH[cc] = xb[8 + cc];
+        }
+    }
+    float acc = 0.0f;
+    for (int bb = b0; bb < b1; bb += D) {
+#pragma unroll
+        for (int s = 0; s < D; s++) {
+            const int b = bb + s;
+            const uint4 h = H[s], q = Q[s];
+            const int nx = b + D < b1 ? b + D : b1 - 1;
+            H[s] = hp[nx];
+            Q[s] = qp[8 * nx];
+            const float4 *xn = xg + 68 * (b + 1 < b1 ? b + 1 : b);
+            float4 NL[4], NH[4];
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++) {
+                NL[cc] = xn[cc];
+                NH[cc] = xn[8 + cc];
+            }
+            if (b < b1) {  // wave-uniform
+                float d = f16_to_f32((uint16_t)(h.x & 0xFFFF)), dmin = f16_to_f32((uint16_t)(h.x >> 16));
+                uint32_t sc_lo, sc_hi, m_lo, m_hi;
+                q4k_scales(h.y, h.z, h.w, sc_lo, sc_hi, m_lo, m_hi);
+                const uint32_t scw = g < 2 ? sc_lo : sc_hi, mw = g < 2 ? m_lo : m_hi;
+                const float d9 = d * 512.0f;  // undoes the 2^-9 of the fp8 reading
+                const float s0 = d9 * ubyte_f(scw, k0), n0 = -(dmin * ubyte_f(mw, k0));
+                const float s1 = d9 * ubyte_f(scw, k1), n1 = -(dmin * ubyte_f(mw, k1));
+                const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+                float pl0 = 0.0f, pl1 = 0.0f, ph0 = 0.0f, ph1 = 0.0f;
+#pragma unroll
+                for (int cc = 0; cc < 4; cc++) {
+                    const uint32_t lo = qw[cc] & 0x0F0F0F0Fu, hi = (qw[cc] >> 4) & 0x0F0F0F0Fu;
+                    float &pl = (cc & 1) ? pl1 : pl0;
+                    float &ph = (cc & 1) ? ph1 : ph0;
+                    fma_nib4(pl, lo, XL[cc]);
+                    fma_nib4(ph, hi, XH[cc]);
+                }
+                const float *sxb = sxg + 16 * b;
+                acc = fmaf(s0, pl0 + pl1, acc);
+                acc = fmaf(n0, sxb[0], acc);
+                acc = fmaf(s1, ph0 + ph1, acc);
+                acc = fmaf(n1, sxb[2], acc);
+            }
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++) {
+                XL[cc] = NL[cc];
+                XH[cc] = NH[cc];
+            }
+        }
+    }
+    if (w & 1) half_part[64 * (w >> 1) + lane] = acc;
+    __syncthreads();
+    if (w & 1) return;
+    acc = acc + half_part[64 * (w >> 1) + lane];
+    acc += __shfl_xor(acc, 1);
+    acc += __shfl_xor(acc, 2);
+    acc += __shfl_xor(acc, 4);
+    if (lane8 == 0 && r < N) c[r] = ACC ? c[r] + acc : acc;
+}
+
+// Host side: the context's scratch for partials and arrival counters (counters start at zero and every
+// launch leaves them at zero). Growing is refused during graph capture.
+int scratch_for(trhip_ctx *ctx, FastScratch &fs, size_t floats, size_t counters) {
+    if (floats <= fs.partial_floats && counters <= fs.ncounters) return TRHIP_OK;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(ctx->stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+        return fail(ctx, TRHIP_ERR_INVALID, "gemv_fast scratch must be sized by an eager call before graph capture");
+    if (floats > fs.partial_floats) {
+        if (fs.partials) { (void)hipStreamSynchronize(ctx->stream); (void)hipFree(fs.partials); }
+        fs.partials = nullptr;
+        hipError_t e = hipMalloc(&fs.partials, floats * sizeof(float));
+        if (e != hipSuccess) { fs.partial_floats = 0; return hip_fail(ctx, e, "gemv_fast partials"); }
+        fs.partial_floats = floats;
+    }
+    if (counters > fs.ncounters) {
+        if (fs.counters) { (void)hipStreamSynchronize(ctx->stream); (void)hipFree(fs.counters); }
+        fs.counters = nullptr;
+        hipError_t e = hipMalloc(&fs.counters, counters * sizeof(int));
+        if (e == hipSuccess) e = hipMemset(fs.counters, 0, counters * sizeof(int));
+        if (e != hipSuccess) { fs.ncounters = 0; return hip_fail(ctx, e, "gemv_fast counters"); }
+        fs.ncounters = counters;
+    }
+    return TRHIP_OK;
+}
+
+template <int D>
+int run_q4k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c, bool acc) {
+    const int64_t nx4 = w->K / 4;
+    size_t lds = (size_t)(nx4 + nx4 / 16) * sizeof(float4) + (size_t)(w->K / 16) * sizeof(float);
+    if (lds > 150 * 1024) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv_fast: K too large for the LDS copy of x");
+    dim3 grid((unsigned)((N + 15) / 16)), block(256);
+    if (acc)
+        hipLaunchKernelGGL((gemv_fast_q4k<true, D>), grid, block, lds, ctx->stream, w->planes(), x, c, N, row0, w->K);
+    else
+        hipLaunchKernelGGL((gemv_fast_q4k<false, D>), grid, block, lds, ctx->stream, w->planes(), x, c, N, row0, w->K);
+    return launch_check(ctx, "gemv_fast_q4k");
+}
+
+}  // namespace
+
 int launch_gemv(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c, bool acc,
                 int mode);
+
 int launch_gemv_fast(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                      bool acc) {
+    if (w->dtype == kQ4K) {
+        // prefetch depth in blocks: TRHIP_FAST_DEPTH overrides (1, 2 or 4)
+        const char *e = getenv("TRHIP_FAST_DEPTH");
+        int dep = e ? atoi(e) : 4;
+        if (dep == 2) return run_q4k<2>(ctx, w, row0, N, x, c, acc);
+        if (dep == 8) return run_q4k<8>(ctx, w, row0, N, x, c, acc);
+        return run_q4k<4>(ctx, w, row0, N, x, c, acc);
+    }
     return launch_gemv(ctx, w, row0, N, x, c, acc, TRHIP_MODE_EXACT);
 }
+
 }  // namespace trhip

@@ -10,10 +10,13 @@
 //   q4_k : hdr[N][nb][16]  d, dmin, scales[12] (block order)  qs[N][nb][128] lane-sliced (see below)
 //   q6_k : ql [N][nb][128] lane-sliced   qh [N][nb][64] lane-sliced   sc [N][nb][16]   d [N][nb] fp16
 //
-// Lane slicing: the exact GEMV gives each of the 4 lanes of a row 8 consecutive elements of every
-// 32-element group (lane t owns sdot32 accumulator t, tensor/cpu_gemv_amd64.s:190-213). The bytes a
-// lane needs are moved next to each other:
-//   q4_k qs  : new[32t + 8g + l]        = old[32g + 8t + l]            (g < 4, l < 8)
+// Lane slicing. q4_k qs: the factored GEMV gives lane (g, h) of a row bytes 32g + 16h .. +16 of every
+// block (low and high nibbles: 16 elements each of sub-blocks 2g and 2g+1); the exact GEMV gives lane
+// t bytes 32g + 8t .. +8 for every g (it owns sdot32 accumulator t, tensor/cpu_gemv_amd64.s:190-213).
+// With 8-byte pieces C(g, t) = old[32g + 8t, +8) stored at 16-byte-slot 4(t>>1) + g, half t&1, the
+// factored lane reads one contiguous 16-byte slice and the exact lane four 8-byte pieces:
+//   q4_k qs  : new[64(t>>1) + 16g + 8(t&1) + l] = old[32g + 8t + l]    (g, t < 4, l < 8)
+// q6_k (exact GEMV lane t owns elements 8t..8t+7 of every 32-element group):
 //   q6_k ql  : new[32t + 16n + 8h + l]  = old[64n + 32h + 8t + l]      (n, h < 2, l < 8)
 //   q6_k qh  : new[16t + 8n + l]        = old[32n + 8t + l]            (n < 2, l < 8)
 #pragma once
@@ -51,8 +54,21 @@ __host__ __device__ constexpr int aux_bytes(int dt) { return dt == kQ4K ? 16 : d
 __host__ __device__ constexpr int sc_bytes(int dt) { return dt == kQ6K ? 16 : 0; }
 __host__ __device__ constexpr int d_bytes(int dt) { return dt == kQ4K ? 0 : 2; }
 
+// Position in a repacked q4_k qs block of original qs byte i = 32g + 8t + l.
+__host__ __device__ constexpr int q4k_pos(int i) {
+    return 64 * ((i >> 4) & 1) + 16 * (i >> 5) + 8 * ((i >> 3) & 1) + (i & 7);
+}
+
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {  // exact for finite values and +-Inf
     return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// Hide a value from the optimizer (no instruction is emitted). Used on a dword-wide nibble mask so the
+// compiler keeps one v_and_b32 per four codes and converts each byte with one v_cvt_f32_ubyte{k},
+// instead of folding the mask into four per-byte bit-field extracts.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
 }
 
 // Byte k (0..3) of a dword as float: v_cvt_f32_ubyte{k}.
@@ -89,7 +105,7 @@ __device__ __forceinline__ float deq_at(const Planes p, int64_t row, int64_t k) 
         if (j < 4) { scv = s[j] & 63; mv = s[j + 4] & 63; }
         else { scv = (uint8_t)((s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4)); mv = (uint8_t)((s[j + 4] >> 4) | ((s[j] >> 6) << 4)); }
         float d = f16_to_f32((uint16_t)(h[0] | (h[1] << 8))), dmin = f16_to_f32((uint16_t)(h[2] | (h[3] << 8)));
-        uint8_t b = p.qs[bi * 128 + 32 * (ee >> 3) + 8 * g + (ee & 7)];
+        uint8_t b = p.qs[bi * 128 + q4k_pos(32 * g + ee)];
         int code = (j & 1) ? (b >> 4) : (b & 0xF);
         return (d * (float)scv) * (float)code - dmin * (float)mv;
     } else {
@@ -106,6 +122,15 @@ __device__ __forceinline__ float deq_at(const Planes p, int64_t row, int64_t k) 
 }  // namespace trhip
 
 // Host-side objects.
+namespace trhip {
+struct FastScratch {  // partial sums and arrival counters of the split-K GEMV (gemv_fast.hip)
+    float *partials = nullptr;
+    size_t partial_floats = 0;
+    int *counters = nullptr;
+    size_t ncounters = 0;
+};
+}  // namespace trhip
+
 struct trhip_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
@@ -114,6 +139,7 @@ struct trhip_ctx {
     void *ws = nullptr;
     size_t ws_bytes = 0;
     int sm_count = 0;
+    trhip::FastScratch fast;
 };
 
 struct trhip_wstore {
@@ -145,7 +171,7 @@ int launch_gemv(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, 
 int launch_gemm_rows(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                      int64_t M, bool acc);
 int launch_quantize_q8(trhip_ctx *ctx, const float *x, int64_t M, int64_t K, int blk, int8_t *q, float *d,
-                       int16_t *bs, int32_t *flags);
+                       int16_t *bs, uint8_t *bad);
 int launch_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
-                int64_t M, bool acc, const int8_t *q, const float *d, const int16_t *bs, const int32_t *flags);
+                int64_t M, bool acc, const int8_t *q, const float *d, const int16_t *bs, const uint8_t *bad);
 }  // namespace trhip

@@ -11,10 +11,6 @@ namespace trhip {
 namespace {
 
 // Destination offset of byte `i` of a q4_k qs block (lane slicing) and of q6_k ql/qh.
-__host__ __device__ inline int q4k_qs_dst(int i) {  // old = 32g + 8t + l -> new = 32t + 8g + l
-    int g = i >> 5, t = (i >> 3) & 3, l = i & 7;
-    return 32 * t + 8 * g + l;
-}
 __host__ __device__ inline int q6k_ql_dst(int i) {  // old = 64n + 32h + 8t + l -> 32t + 16n + 8h + l
     int n = i >> 6, h = (i >> 5) & 1, t = (i >> 3) & 3, l = i & 7;
     return 32 * t + 16 * n + 8 * h + l;
@@ -43,7 +39,7 @@ __global__ void repack_kernel(const uint8_t *__restrict__ raw, uint8_t *__restri
     } else if (DT == kQ4K) {
         uint8_t *h = aux + bi * 16;
         for (int i = 0; i < 16; i++) mv(h + i, rb + i);
-        for (int i = 0; i < 128; i++) mv(q + q4k_qs_dst(i), rb + 16 + i);
+        for (int i = 0; i < 128; i++) mv(q + q4k_pos(i), rb + 16 + i);
     } else {  // q6_k: ql[128] qh[64] sc[16] d[2]
         uint8_t *h = aux + bi * 64, *s = sc + bi * 16;
         uint8_t *dd = reinterpret_cast<uint8_t *>(d + bi);
@@ -88,8 +84,7 @@ __device__ void dequant_group(const Planes p, int64_t bi, int G, float *y) {
         const uint8_t *q = p.qs + bi * 128;
         int g = j >> 1;
         for (int e = 0; e < 32; e++) {
-            int t = e >> 3, l = e & 7;
-            uint8_t b = q[32 * t + 8 * g + l];  // old byte 32g + e
+            uint8_t b = q[q4k_pos(32 * g + e)];  // old byte 32g + e
             uint32_t code = (j & 1) ? (b >> 4) : (b & 0xF);
             y[e] = d1 * (float)code - m1;
         }

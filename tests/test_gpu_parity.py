@@ -293,3 +293,52 @@ def test_store_refuses_bad_scale(backend):
     with pytest.raises(TrhipError) as e:
         backend.FromQuantized(Q8, raw, 3, 32)
     assert e.value.code == 7
+
+
+# ---------------------------------------------------------------- fast mode (tolerance-bound)
+FAST_TOL = {Q8: 1e-5, Q4: 1e-5, Q4K: 1e-4, Q6K: 1e-4}  # north star: 1e-5, 1e-4 for K-quants
+
+
+@pytest.mark.parametrize("dt", DTS)
+@pytest.mark.parametrize("N,K", [(7, 256), (64, 512), (130, 2048), (33, 4096), (200, 14336), (1024, 4096)])
+def test_gemv_fast_tolerance(backend, dt, N, K):
+    """MODE_FAST: |gpu - oracle| / (1 + |oracle|) within the north-star bound, for accumulate and set,
+    on encoded N(0, 0.02) weights with 1% outliers and on x1000 activations."""
+    raw = synth.quant_weights(dt, N, K, seed=N + K, outliers=0.01)
+    w = backend.FromQuantized(dt, raw, N, K)
+    for scale, acc in ((1.0, False), (1000.0, True)):
+        x = synth.activations(1, K, seed=K) * np.float32(scale)
+        c0 = synth.activations(1, N, seed=N).reshape(-1)
+        xb, cb = backend.ctx.to_device(x), backend.ctx.to_device(c0)
+        if acc:
+            backend.Gemm(1, N, K, xb, w, cb, mode=MODE_FAST)
+        else:
+            backend.GemmSet(1, N, K, xb, w, cb, mode=MODE_FAST)
+        got = cb.download(np.float32, N)
+        want = O.quant_gemm(dt, 1, N, K, x, raw, c0 if acc else None).reshape(-1)
+        err = rel_err(got / scale, want / scale)
+        assert err <= FAST_TOL[dt], (dt, N, K, scale, err)
+        for b in (xb, cb):
+            b.free()
+    w.release()
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_gemv_fast_deterministic_and_sliced(backend, dt):
+    """Same input, same bits on every call (no atomic accumulation; TestQuantGemvIsDeterministic), and a
+    row slice computes the slice's rows."""
+    N, K = 300, 14336 if dt in (Q4K, Q6K) else 4096
+    raw = synth.quant_weights(dt, N, K, seed=5, outliers=0.01)
+    w = backend.FromQuantized(dt, raw, N, K)
+    x = synth.activations(1, K, seed=6)
+    xb, cb = backend.ctx.to_device(x), backend.ctx.alloc(N * 4)
+    backend.GemmSet(1, N, K, xb, w, cb, mode=MODE_FAST)
+    first = cb.download(np.float32, N)
+    for _ in range(3):
+        backend.GemmSet(1, N, K, xb, w, cb, mode=MODE_FAST)
+        same_bits(cb.download(np.float32, N), first)
+    backend.GemmSet(1, 100, K, xb, w, cb, row0=123, mode=MODE_FAST)
+    same_bits(cb.download(np.float32, 100), first[123:223])
+    for b in (xb, cb):
+        b.free()
+    w.release()
