@@ -23,7 +23,8 @@ namespace {
 template <int BLK>
 __global__ __launch_bounds__(256) void quantize_q8_kernel(const float *__restrict__ x, int64_t M, int64_t K,
                                                           int8_t *__restrict__ q, float *__restrict__ d,
-                                                          int16_t *__restrict__ bs, uint8_t *__restrict__ bad_blk) {
+                                                          int16_t *__restrict__ bs, uint8_t *__restrict__ bad_blk,
+                                                          uint16_t *__restrict__ sj) {
     constexpr int TPB = BLK / 4;  // threads per activation block
     const int64_t nbk = K / BLK;
     const int64_t gt = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -72,27 +73,20 @@ __global__ __launch_bounds__(256) void quantize_q8_kernel(const float *__restric
     s16 += __shfl_xor(s16, 1);
     s16 += __shfl_xor(s16, 2);
     if ((l4 & 3) == 0) bs[off / 16] = (int16_t)s16;
+    if (BLK == 256 && sj) {
+        // 32-element sums S_j = 64*Sh + Sl (Sh = floor(S/64) in [-64, 63], Sl in [0, 63]) as f16 operands of the
+        // q4_k prefill kernel's msum product: [Sh_0..Sh_7, Sl_0..Sl_7] per activation block.
+        const int s32 = s16 + __shfl_xor(s16, 4);
+        if ((l4 & 7) == 0) {
+            const int j = l4 >> 3, sh = s32 >> 6, sl = s32 & 63;
+            sj[blk_id * 16 + j] = __builtin_bit_cast(uint16_t, (_Float16)(float)sh);
+            sj[blk_id * 16 + 8 + j] = __builtin_bit_cast(uint16_t, (_Float16)(float)sl);
+        }
+    }
 }
 
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
-}
-
-// Exact fp32 dot of activation row xr with weight row `row` in sdot32 order (fallback for rows with
-// NaN/Inf; one thread, 32 chains).
-template <int DT>
-__device__ float exact_dot_row(const Planes p, int64_t row, const float *__restrict__ xr, int64_t K) {
-    float acc[32];
-#pragma unroll
-    for (int l = 0; l < 32; l++) acc[l] = 0.0f;
-    for (int64_t k0 = 0; k0 < K; k0 += 32)
-#pragma unroll
-        for (int l = 0; l < 32; l++) acc[l] = fmaf(xr[k0 + l], deq_at<DT>(p, row, k0 + l), acc[l]);
-    float Y[8];
-#pragma unroll
-    for (int l = 0; l < 8; l++) Y[l] = (acc[l] + acc[8 + l]) + (acc[16 + l] + acc[24 + l]);
-    float s0 = Y[0] + Y[4], s1 = Y[1] + Y[5], s2 = Y[2] + Y[6], s3 = Y[3] + Y[7];
-    return (s0 + s2) + (s1 + s3);
 }
 
 // One thread per output (m, n); blocks in order. Correct for every M; the int8-MFMA kernel
@@ -217,26 +211,31 @@ int run_valu(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, con
 }  // namespace
 
 int launch_quantize_q8(trhip_ctx *ctx, const float *x, int64_t M, int64_t K, int blk, int8_t *q, float *d, int16_t *bs,
-                       uint8_t *bad) {
+                       uint8_t *bad, uint16_t *sj) {
     if (M == 0 || K == 0) return TRHIP_OK;
     int64_t total = M * K / 4;
     dim3 grid((unsigned)((total + 255) / 256)), block(256);
     if (blk == 256)
-        hipLaunchKernelGGL(quantize_q8_kernel<256>, grid, block, 0, ctx->stream, x, M, K, q, d, bs, bad);
+        hipLaunchKernelGGL(quantize_q8_kernel<256>, grid, block, 0, ctx->stream, x, M, K, q, d, bs, bad, sj);
     else
-        hipLaunchKernelGGL(quantize_q8_kernel<32>, grid, block, 0, ctx->stream, x, M, K, q, d, bs, bad);
+        hipLaunchKernelGGL(quantize_q8_kernel<32>, grid, block, 0, ctx->stream, x, M, K, q, d, bs, bad, nullptr);
     return launch_check(ctx, "quantize_q8");
 }
 
+// Below this many activation rows the thread-per-output kernel wins (the MFMA tile is 128 rows).
+constexpr int64_t kActqMfmaMinRows = 8;
+
 int launch_actq_mfma(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
-                     int64_t M, bool acc, const int8_t *q, const float *d, const int16_t *bs, const uint8_t *bad);
+                     int64_t M, bool acc, const int8_t *q, const float *d, const uint16_t *sj, const uint8_t *bad);
 
 int launch_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c, int64_t M,
-                bool acc, const int8_t *q, const float *d, const int16_t *bs, const uint8_t *bad) {
+                bool acc, const int8_t *q, const float *d, const int16_t *bs, const uint8_t *bad, const uint16_t *sj) {
     if (N == 0 || M == 0) return TRHIP_OK;
     switch (w->dtype) {
     case kQ4: return run_valu<kQ4>(ctx, w, row0, N, x, c, M, acc, q, d, bs, bad);
-    case kQ4K: return run_valu<kQ4K>(ctx, w, row0, N, x, c, M, acc, q, d, bs, bad);
+    case kQ4K:
+        if (M >= kActqMfmaMinRows && sj) return launch_actq_mfma(ctx, w, row0, N, x, c, M, acc, q, d, sj, bad);
+        return run_valu<kQ4K>(ctx, w, row0, N, x, c, M, acc, q, d, bs, bad);
     case kQ6K: return run_valu<kQ6K>(ctx, w, row0, N, x, c, M, acc, q, d, bs, bad);
     }
     return fail(ctx, TRHIP_ERR_UNSUPPORTED, "actq: dtype must be q4, q4_k or q6_k");

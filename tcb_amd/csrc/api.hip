@@ -415,7 +415,7 @@ int trhip_quantize_q8(trhip_ctx *ctx, const float *x, int64_t M, int64_t K, int 
     int st = TRHIP_OK;
     uint8_t *bad = static_cast<uint8_t *>(workspace(ctx, (size_t)(M * (K / blk)), &st));
     if (!bad) return st;
-    return launch_quantize_q8(ctx, x, M, K, blk, q, d, bs, bad);
+    return launch_quantize_q8(ctx, x, M, K, blk, q, d, bs, bad, nullptr);
 }
 
 int trhip_gemm_q_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
@@ -437,7 +437,8 @@ int trhip_gemm_q_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64
     size_t o_d = align_up(o_q + (size_t)(M * K), 256);
     size_t o_bs = align_up(o_d + (size_t)(M * nb) * sizeof(float), 256);
     size_t o_fl = align_up(o_bs + (size_t)(M * (K / 16)) * sizeof(int16_t), 256);
-    size_t o_x = align_up(o_fl + (size_t)(M * nb), 256);
+    size_t o_sj = align_up(o_fl + (size_t)(M * nb), 256);
+    size_t o_x = align_up(o_sj + (w->dtype == TRHIP_Q4K ? (size_t)(M * nb) * 32 : 0), 256);
     bool copy_x = reinterpret_cast<uintptr_t>(x) % 16 != 0;
     size_t total = o_x + (copy_x ? (size_t)(M * K) * sizeof(float) : 0);
     int st = TRHIP_OK;
@@ -447,6 +448,7 @@ int trhip_gemm_q_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64
     float *d = reinterpret_cast<float *>(ws + o_d);
     int16_t *bs = reinterpret_cast<int16_t *>(ws + o_bs);
     uint8_t *bad = ws + o_fl;  // one flag byte per activation block (NaN/Inf present)
+    uint16_t *sj = w->dtype == TRHIP_Q4K ? reinterpret_cast<uint16_t *>(ws + o_sj) : nullptr;  // q4_k msum operands
     const float *xa = x;
     if (copy_x) {
         float *tmp = reinterpret_cast<float *>(ws + o_x);
@@ -454,8 +456,8 @@ int trhip_gemm_q_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64
         if (e != hipSuccess) return hip_fail(ctx, e, "gemm_q_actq: align x");
         xa = tmp;
     }
-    if ((st = launch_quantize_q8(ctx, xa, M, K, blk, q, d, bs, bad)) != TRHIP_OK) return st;
-    return launch_actq(ctx, w, row0, N, xa, c, M, accumulate != 0, q, d, bs, bad);
+    if ((st = launch_quantize_q8(ctx, xa, M, K, blk, q, d, bs, bad, sj)) != TRHIP_OK) return st;
+    return launch_actq(ctx, w, row0, N, xa, c, M, accumulate != 0, q, d, bs, bad, sj);
 }
 
 int trhip_open_q(trhip_ctx *ctx, const trhip_wstore *w, int64_t elem_off, int64_t n, float *out) {

@@ -119,6 +119,23 @@ __device__ __forceinline__ float deq_at(const Planes p, int64_t row, int64_t k) 
     }
 }
 
+// Exact fp32 dot of activation row xr with weight row `row` in sdot32 order (fallback for rows with
+// NaN/Inf; one thread, 32 chains).
+template <int DT>
+__device__ __forceinline__ float exact_dot_row(const Planes p, int64_t row, const float *__restrict__ xr, int64_t K) {
+    float acc[32];
+#pragma unroll
+    for (int l = 0; l < 32; l++) acc[l] = 0.0f;
+    for (int64_t k0 = 0; k0 < K; k0 += 32)
+#pragma unroll
+        for (int l = 0; l < 32; l++) acc[l] = fmaf(xr[k0 + l], deq_at<DT>(p, row, k0 + l), acc[l]);
+    float Y[8];
+#pragma unroll
+    for (int l = 0; l < 8; l++) Y[l] = (acc[l] + acc[8 + l]) + (acc[16 + l] + acc[24 + l]);
+    float s0 = Y[0] + Y[4], s1 = Y[1] + Y[5], s2 = Y[2] + Y[6], s3 = Y[3] + Y[7];
+    return (s0 + s2) + (s1 + s3);
+}
+
 }  // namespace trhip
 
 // Host-side objects.
@@ -171,7 +188,8 @@ int launch_gemv(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, 
 int launch_gemm_rows(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                      int64_t M, bool acc);
 int launch_quantize_q8(trhip_ctx *ctx, const float *x, int64_t M, int64_t K, int blk, int8_t *q, float *d,
-                       int16_t *bs, uint8_t *bad);
+                       int16_t *bs, uint8_t *bad, uint16_t *sj);
 int launch_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
-                int64_t M, bool acc, const int8_t *q, const float *d, const int16_t *bs, const uint8_t *bad);
+                int64_t M, bool acc, const int8_t *q, const float *d, const int16_t *bs, const uint8_t *bad,
+                const uint16_t *sj);
 }  // namespace trhip

@@ -249,6 +249,34 @@ def test_actq_keeps_non_finite(backend, dt, bad):
     w.release()
 
 
+@pytest.mark.parametrize("M,N,K,row0,acc", [(8, 64, 256, 0, True), (130, 70, 512, 0, False), (257, 33, 1024, 5, True),
+                                            (16, 200, 4096, 0, True), (128, 128, 256, 64, False), (300, 1, 512, 0, True)])
+def test_actq_tiles_bits(backend, M, N, K, row0, acc):
+    """Row counts that fill, straddle and overhang the 128 x 64 tiles of the MFMA prefill kernel, ragged N, a row
+    slice of the store, both accumulate modes, x1000 / zero / +-1 rows and one NaN row inside a tile."""
+    rng = _rng(M * 7 + N * 3 + K + row0)
+    raw = _weights(Q4K, row0 + N, K, M + N + K)
+    X = _x(rng, M * K).reshape(M, K)
+    for m in range(M):
+        if m % 7 == 1:
+            X[m] *= 1000
+        elif m % 7 == 2:
+            X[m, :256] = 0
+        elif m % 7 == 3:
+            X[m] = 1 - 2 * (np.arange(K) % 2)
+    if M > 20:
+        X[M // 2, 3] = np.nan
+    w = backend.FromQuantized(Q4K, raw, row0 + N, K)
+    c0 = _x(rng, M * N) if acc else np.zeros(M * N, np.float32)
+    xb, cb = backend.ctx.to_device(X), backend.ctx.to_device(c0)
+    backend.GemmActQuant(M, N, K, xb, w, cb, row0=row0, accumulate=acc)
+    rows = raw.reshape(row0 + N, -1)[row0:]
+    same_bits(cb.download(np.float32, M * N), O.quant_gemm_act(Q4K, M, N, K, X, np.ascontiguousarray(rows), c0))
+    for b in (xb, cb):
+        b.free()
+    w.release()
+
+
 @pytest.mark.parametrize("dt,N,K,M", [(Q4K, 14336, 4096, 16), (Q4K, 4096, 14336, 8), (Q6K, 1024, 4096, 32),
                                       (Q4, 4096, 4096, 16)])
 def test_actq_llama_shapes_bits(backend, dt, N, K, M):
