@@ -1,0 +1,122 @@
+"""CPU tests of the boundary and host logic: the C-ABI library loads and exports every entry point that
+include/trhip.h declares, the Python binding covers the same set, error paths fail loudly, and the synthetic
+encoders used by the benchmark produce well-formed blocks. No compute call is made (there is no GPU here)."""
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "trhip.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(trhip_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    names = declared()
+    for must in ("trhip_init", "trhip_wstore_create", "trhip_gemm_q", "trhip_gemm_q_actq", "trhip_open_q",
+                 "trhip_embedding_q", "trhip_check_quant_scales", "trhip_strerror", "trhip_last_error"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    from tcb_amd import _lib
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in declared() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_binding_covers_the_header():
+    from tcb_amd import _lib
+    assert sorted(n for n, _, _ in _lib.SIGNATURES) == declared()
+
+
+def test_error_strings_and_version():
+    from tcb_amd import _lib
+    lib = _lib.lib()
+    assert lib.trhip_version() > 0
+    for code in range(0, 8):
+        s = lib.trhip_strerror(code)
+        assert s and len(s) >= 2
+    assert b"unknown" in lib.trhip_strerror(999).lower()
+
+
+def test_check_quant_scales_abi_matches_oracle():
+    """trhip_check_quant_scales runs on the host (load gate, quant.go:108-128): same answer as the oracle."""
+    from tcb_amd import _lib
+    lib = _lib.lib()
+    for dt in (1, 2, 3, 4):
+        size = O.BLOCK[dt][1]
+        for at in {1: [0], 2: [0], 3: [0, 2], 4: [208]}[dt]:
+            raw = np.zeros(4 * size, np.uint8)
+            raw[2 * size + at], raw[2 * size + at + 1] = 0x00, 0x7C
+            bad = ctypes.c_int64(0)
+            assert lib.trhip_check_quant_scales(dt, raw.ctypes.data_as(ctypes.c_void_p), raw.size, ctypes.byref(bad)) == 0
+            assert bad.value == 2 == O.check_quant_scales(dt, raw)
+    bad = ctypes.c_int64(0)
+    assert lib.trhip_check_quant_scales(9, None, 0, ctypes.byref(bad)) != 0
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    from tcb_amd import _lib
+    with pytest.raises(ImportError):
+        _lib.load(str(tmp_path / "libtrhip.so"))
+
+
+def test_null_context_is_refused():
+    from tcb_amd import _lib
+    lib = _lib.lib()
+    assert lib.trhip_gemm_q(None, None, 0, 1, None, None, 1, 32, 1, 0) != 0
+    assert lib.trhip_gemm_q_actq(None, None, 0, 1, None, None, 1, 256, 1) != 0
+    assert lib.trhip_sync(None) != 0
+
+
+def test_bench_refuses_more_than_one_gpu():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 2
+    assert "one" in r.stderr.lower()
+
+
+# ---------------------------------------------------------------- synthetic encoders (benchmark inputs)
+def test_q4_0_encoder_zero_block():
+    """llama.cpp quantize_row_q4_0_ref on a zero block: d = -0/8 = -0 (fp16 0x8000), codes 8 (0x88)."""
+    from tcb_amd import synth
+    raw = synth.encode_q4_0(np.zeros((1, 32), np.float32))
+    assert list(raw[:2]) == [0x00, 0x80]
+    assert np.all(raw[2:] == 0x88)
+    assert np.all(O.dequant(2, raw) == 0)
+
+
+def test_q8_0_encoder_known_block():
+    """d = amax/127 (fp16), code = round-half-away(x/d)."""
+    from tcb_amd import synth
+    x = np.zeros((1, 32), np.float32)
+    x[0, 0], x[0, 1], x[0, 2] = 127.0, -63.5, 0.5
+    raw = synth.encode_q8_0(x)
+    assert list(raw[:2]) == [0x00, 0x3C]  # d = 1.0
+    assert raw[2:5].view(np.int8).tolist() == [127, -64, 1]
+
+
+@pytest.mark.parametrize("dt,bound", [(1, 0.008), (2, 0.1), (3, 0.1), (4, 0.025)])
+def test_encoders_round_trip(dt, bound):
+    """Encoded then dequantized (golden-pinned dequant) stays within the format's error: relative RMS bound."""
+    from tcb_amd import synth
+    N, K = 8, 1024
+    x = synth.weights_f32(N, K, seed=5)  # Gaussian; 1% x10 outliers would widen every bound
+    raw = {1: synth.encode_q8_0, 2: synth.encode_q4_0, 3: synth.encode_q4_k, 4: synth.encode_q6_k}[dt](x)
+    assert raw.size == N * K // O.BLOCK[dt][0] * O.BLOCK[dt][1]
+    assert O.check_quant_scales(dt, raw) == -1
+    y = O.dequant(dt, raw).reshape(N, K)
+    err = np.sqrt(np.mean((y.astype(np.float64) - x) ** 2)) / np.sqrt(np.mean(x.astype(np.float64) ** 2))
+    assert err < bound, err
