@@ -14,6 +14,10 @@ device, int32 block sums, fp32 epilogue) in int8 TOPS = 2*M*N*K / time, and the 
 restatement of the reference's sdotq4k path (oracle/trq_avx2.c), all host cores, on the same bytes.
 
 Prints one JSON line. --gpus N > 1 exits: this build runs on one GPU.
+
+--profile-kernel {gemv,prefill,copy} runs only that kernel, eagerly, --steps times (for rocprofv3 counter runs):
+gemv = the headline GEMV over the cold ring, prefill = one act-quant GEMM per step, copy = a plain device copy of
+COPY_BYTES (torch) that calibrates the FETCH_SIZE / WRITE_SIZE counters.
 """
 import argparse
 import json
@@ -31,6 +35,14 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, datasheet
 INT8_PEAK_TOPS = 5033.0      # MI355X dense int8 MFMA, datasheet (5.03 POPS)
 N, K = 14336, 4096
 RING_BYTES = int(1.1 * (1 << 30))
+COPY_BYTES = 256 << 20
+
+# HBM bytes per launch of the headline kernel from rocprofv3 FETCH_SIZE + WRITE_SIZE over --profile-kernel gemv,
+# each divided by the same counter's reading per byte of the calibration copy (profiles/gemv_q4_k_14336x4096_*.txt).
+# Keyed by mode.
+TRAFFIC = {"fast": 33278109, "exact": 33434768}
+# Same counters over --profile-kernel prefill (profiles/prefill_q4_k_14336x4096_M512.txt): quantizer + MFMA kernel.
+PREFILL_TRAFFIC = {"quantize_q8": 11181340, "actq_mfma_q4k": 100162620}
 
 
 def algorithmic_bytes(n, k):
@@ -47,7 +59,47 @@ def parse():
                     help="headline mode; the other mode is measured and reported beside it")
     ap.add_argument("--prefill-m", type=int, default=512)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample (0 = skip)")
+    ap.add_argument("--profile-kernel", choices=["gemv", "prefill", "copy"], default=None,
+                    help="run only this kernel --steps times, eagerly (counter runs)")
     return ap.parse_args()
+
+
+def profile_kernel(a):
+    """One kernel, --steps eager launches, nothing else timed or printed but one JSON line."""
+    import numpy as np
+    from tcb_amd import MODE_EXACT, MODE_FAST, Q4K, QuantBackend, synth
+    if a.profile_kernel == "copy":
+        import torch
+        src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(a.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"profiled": "copy", "launches": a.steps, "bytes_read": COPY_BYTES, "bytes_written": COPY_BYTES}))
+        return 0
+    tb = QuantBackend(0)
+    raw = synth.quant_weights(Q4K, N, K, seed=3, outliers=0.01)
+    if a.profile_kernel == "gemv":
+        ring = [tb.FromQuantized(Q4K, raw, N, K) for _ in range(max(2, -(-RING_BYTES // raw.nbytes)))]
+        xb = tb.ctx.to_device(synth.activations(1, K, seed=4))
+        cb = tb.ctx.alloc(N * 4)
+        mode = MODE_FAST if a.mode == "fast" else MODE_EXACT
+        for i in range(a.steps):
+            tb.GemmSet(1, N, K, xb, ring[i % len(ring)], cb, mode=mode)
+        tb.ctx.sync()
+        print(json.dumps({"profiled": "gemv_q4_k_%s" % a.mode, "launches": a.steps,
+                          "algorithmic_bytes": algorithmic_bytes(N, K)}))
+    else:
+        M = a.prefill_m
+        w = tb.FromQuantized(Q4K, raw, N, K)
+        Xb = tb.ctx.to_device(synth.activations(M, K, seed=5))
+        Cb = tb.ctx.alloc(M * N * 4)
+        for _ in range(a.steps):
+            tb.GemmActQuant(M, N, K, Xb, w, Cb, accumulate=False)
+        tb.ctx.sync()
+        print(json.dumps({"profiled": "prefill_q4_k_M%d" % M, "launches": a.steps, "ops": 2 * M * N * K}))
+    tb.close()
+    return 0
 
 
 def time_graph(tb, graph, replays):
@@ -89,6 +141,8 @@ def main():
         print("bench.py: this build measures one MI355X; multi-GPU runs (--gpus %d) are not part of it." % a.gpus,
               file=sys.stderr)
         return 2
+    if a.profile_kernel:
+        return profile_kernel(a)
     from tcb_amd import MODE_EXACT, MODE_FAST, Q4K, QuantBackend, _lib, synth
 
     mode = MODE_FAST if a.mode == "fast" else MODE_EXACT
@@ -149,7 +203,8 @@ def main():
         tops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
         prefill = {"workload": "act-quant GEMM q4_k %dx%d, M=%d (quantize + int block sums + fp32 epilogue)" % (N, K, M),
                    "us": round(ms * 1e3, 2), "int8_tops": round(tops, 2),
-                   "frac_of_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+                   "frac_of_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                   "traffic_bytes": PREFILL_TRAFFIC if M == 512 else None}
         Xb.free()
         Cb.free()
 
@@ -202,7 +257,7 @@ def main():
         other_name + "_mode": {"us_per_gemv": round(us_other, 3), "GB/s": round(abytes / (us_other * 1e-6) / 1e9, 1),
                                "warm_us_per_gemv": round(us_other_warm, 3)},
         "roofline": {"bound": "hbm", "achieved": round(gbs_cold, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs_cold / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs_cold / HBM_PEAK_GBS, 4), "traffic": TRAFFIC.get(a.mode),
                      "kernel": "gemv_q4_k_%s" % a.mode, "algorithmic_bytes_per_launch": abytes},
         "prefill": prefill,
         "cpu_baseline": cpu,

@@ -240,9 +240,12 @@ int launch_gemv(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, 
 int launch_gemv_fast(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                      bool acc) {
     if (w->dtype == kQ4K) {
-        // prefetch depth in blocks: TRHIP_FAST_DEPTH overrides (1, 2 or 4)
-        const char *e = getenv("TRHIP_FAST_DEPTH");
-        int dep = e ? atoi(e) : 4;
+        // blocks in flight per lane: 2 measured fastest on the 14336x4096 cold ring; TRHIP_FAST_DEPTH (2, 4 or 8)
+        // overrides
+        static const int dep = [] {
+            const char *e = getenv("TRHIP_FAST_DEPTH");
+            return e ? atoi(e) : 2;
+        }();
         if (dep == 2) return run_q4k<2>(ctx, w, row0, N, x, c, acc);
         if (dep == 8) return run_q4k<8>(ctx, w, row0, N, x, c, acc);
         return run_q4k<4>(ctx, w, row0, N, x, c, acc);
