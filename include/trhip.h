@@ -115,7 +115,8 @@ int trhip_gemm_q(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N,
 
 /* ActQuantGemmer.GemmActQuant (tensor/matmul.go:59-61, tensor/cpu_dtype.go:438-446 ->
  * tensor/cpu_quant_q8.go:125-259): x rows are quantized on the device to Q8 blocks of the
- * weight's block size (quantizeQ8), integer block sums run on int8 MFMA, and the per-block
+ * weight's block size (quantizeQ8), integer block sums are exact int32 (int8 MFMA for q4_k with
+ * M >= 8, packed int8 dot products otherwise), and the per-block
  * fp32 epilogue follows the reference order, so outputs are bit-identical to the CPU path.
  * Rows holding NaN/Inf use the fp32 path for that row only. dtype must be q4, q4_k or q6_k
  * (QuantActSupported, tensor/cpu_quant_q8.go:122), else TRHIP_ERR_UNSUPPORTED. */
@@ -128,8 +129,9 @@ int trhip_gemm_q_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64
 int trhip_open_q(trhip_ctx *ctx, const trhip_wstore *w, int64_t elem_off, int64_t n, float *out);
 
 /* Backend.Embedding for a quantized table (tensor/device.go:482, tensor/cpu_quant.go:163-171):
- * out[i, :] = deq(w)[idx[i], :]; idx is a device array of nidx int64 row indices. Indices are
- * checked on the device; an out-of-range index returns TRHIP_ERR_INVALID (H3043). */
+ * out[i, :] = deq(w)[idx[i], :]; idx is a host array of nidx int64 row indices (the reference passes
+ * a Go []int). Indices are checked on the host before upload; an out-of-range index returns
+ * TRHIP_ERR_INVALID (H3043). The call waits until the indices are on the device. */
 int trhip_embedding_q(trhip_ctx *ctx, const trhip_wstore *w, const int64_t *idx, int64_t nidx, float *out);
 
 /* Quantize fp32 rows to Q8 activation blocks on the device (tensor/cpu_quant_q8.go:39-68):

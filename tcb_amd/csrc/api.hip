@@ -151,8 +151,6 @@ int trhip_destroy(trhip_ctx *ctx) {
     DevGuard g(ctx);
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->ws) (void)hipFree(ctx->ws);
-    if (ctx->fast.partials) (void)hipFree(ctx->fast.partials);
-    if (ctx->fast.counters) (void)hipFree(ctx->fast.counters);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return TRHIP_OK;
@@ -421,7 +419,7 @@ int trhip_quantize_q8(trhip_ctx *ctx, const float *x, int64_t M, int64_t K, int 
 int trhip_gemm_q_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                       int64_t M, int64_t K, int accumulate) {
     if (!ctx || !w) return TRHIP_ERR_INVALID;
-    if (w->dtype == TRHIP_Q8) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemm_q_actq: q8 weights are not supported (H6724)");
+    if (w->dtype == TRHIP_Q8) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemm_q_actq: q8 weights are not supported (H6723)");
     if (M < 0 || N < 0 || row0 < 0 || row0 + N > w->N || K != w->K)
         return fail(ctx, TRHIP_ERR_INVALID, "gemm_q_actq: shape does not match the store");
     if (M == 0 || N == 0) return TRHIP_OK;

@@ -1,71 +1,20 @@
-// gemv_fast.hip -- decode GEMV (M == 1) in factored order: within the north-star tolerance
-// (|a-b|/(1+|b|) <= 1e-5, 1e-4 for K-quants), not bit-identical to TR's CPU path.
+// gemv_fast.hip -- decode GEMV (M == 1) in factored order: within the tolerance the reference allows a
+// device GEMV (|a-b|/(1+|b|) <= 1e-5, 1e-4 for K-quants), not bit-identical to TR's CPU path.
 //
-// Per 32-element sub-block j (16 for q6_k) with value y = s_j*q - m_j (tensor/quant.go:139-205):
+// Per 32-element sub-block j with value y = s_j*q - m_j (tensor/quant.go:167-182):
 //   sum_e y_e x_e = s_j * (sum_e q_e x_e) - m_j * (sum_e x_e)
-// so the inner loop is one convert and one fused multiply-add per weight. The x sums are the same for
-// every row and are computed once per workgroup into LDS.
+// so the inner loop is one convert and one fused multiply-add per weight. The 16-element sums of x are the
+// same for every row and are computed once per workgroup into LDS next to x.
 //
-// Mapping: a wave is 64 rows (lane = row), all lanes on the same block, so x is wave-uniform and is
-// read with scalar loads. A workgroup is 64 rows x WAVES waves; wave w takes BPW consecutive blocks; a
-// grid column (blockIdx.y) takes WAVES*BPW blocks. Partial sums are combined in a fixed order: the
-// waves of a workgroup through LDS, the workgroups of a row tile through a partials buffer summed by
-// whichever workgroup arrives last (integer arrival counter, reset by that workgroup). No float atomics,
-// so the result depends only on the shape (the reference forbids atomic accumulation on this path,
-// gpu/kernel_quant_gemv.go:14-16).
+// Every partial sum is combined in a fixed order inside one workgroup (LDS, then a fixed xor-butterfly),
+// with no atomics, so the result depends only on the shape (the reference forbids atomic accumulation on
+// this path, gpu/kernel_quant_gemv.go:14-16). q4_k only; the other dtypes use the exact kernel.
 #include "trhip_internal.hpp"
 
 #include <cstdlib>
 
 namespace trhip {
 namespace {
-
-constexpr int kWaves = 4;
-
-template <int k>
-__device__ __forceinline__ float ub(uint32_t v) { return ubyte_f(v, k); }
-
-// x sums for this workgroup's blocks: sx[i] = sum of x over 16-element group i (relative to k0).
-__device__ __forceinline__ void x_sums16(float *sx, const float *__restrict__ x, int64_t k0, int ngroups) {
-    for (int i = threadIdx.x; i < ngroups; i += blockDim.x) {
-        const float4 *p = reinterpret_cast<const float4 *>(x + k0 + 16 * (int64_t)i);
-        float4 a = p[0], b = p[1], c = p[2], d = p[3];
-        sx[i] = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w)) + ((c.x + c.y) + (c.z + c.w)) +
-                ((d.x + d.y) + (d.z + d.w));
-    }
-}
-
-// Fixed-order reduction of the WAVES partials per row inside the workgroup, then across grid columns.
-template <bool ACC>
-__device__ __forceinline__ void finish(float part, float *lds_part, float *__restrict__ c, float *__restrict__ partials,
-                                       int *__restrict__ counters, int64_t N, int64_t r, int ncol) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    lds_part[w * 64 + lane] = part;
-    __syncthreads();
-    if (w != 0) return;
-    float s = lds_part[lane];
-#pragma unroll
-    for (int i = 1; i < kWaves; i++) s = s + lds_part[i * 64 + lane];
-    if (ncol == 1) {
-        if (r < N) c[r] = ACC ? c[r] + s : s;
-        return;
-    }
-    if (r < N) partials[(int64_t)blockIdx.y * N + r] = s;
-    __shared__ int last;
-    __threadfence();  // our partials are visible device-wide before we count ourselves in
-    // one arrival per workgroup; the last one to arrive sums every column in column order
-    if (lane == 0) {
-        int old = __hip_atomic_fetch_add(counters + blockIdx.x, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        last = (old == ncol - 1);
-        if (last) __hip_atomic_store(counters + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __builtin_amdgcn_wave_barrier();
-    __threadfence();
-    if (!last || r >= N) return;
-    float t = __hip_atomic_load(partials + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    for (int i = 1; i < ncol; i++) t = t + __hip_atomic_load(partials + (int64_t)i * N + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    c[r] = ACC ? c[r] + t : t;
-}
 
 // ---------------------------------------------------------------- q4_k
 // Nibble pairs to floats: a byte holding 0..15, read as an OCP FP8 E4M3 value, is exactly q * 2^-9
@@ -192,31 +141,6 @@ __global__ __launch_bounds__(256) void gemv_fast_q4k(const Planes p, const float
     acc += __shfl_xor(acc, 2);
     acc += __shfl_xor(acc, 4);
     if (lane8 == 0 && r < N) c[r] = ACC ? c[r] + acc : acc;
-}
-
-// Host side: the context's scratch for partials and arrival counters (counters start at zero and every
-// launch leaves them at zero). Growing is refused during graph capture.
-int scratch_for(trhip_ctx *ctx, FastScratch &fs, size_t floats, size_t counters) {
-    if (floats <= fs.partial_floats && counters <= fs.ncounters) return TRHIP_OK;
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(ctx->stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
-        return fail(ctx, TRHIP_ERR_INVALID, "gemv_fast scratch must be sized by an eager call before graph capture");
-    if (floats > fs.partial_floats) {
-        if (fs.partials) { (void)hipStreamSynchronize(ctx->stream); (void)hipFree(fs.partials); }
-        fs.partials = nullptr;
-        hipError_t e = hipMalloc(&fs.partials, floats * sizeof(float));
-        if (e != hipSuccess) { fs.partial_floats = 0; return hip_fail(ctx, e, "gemv_fast partials"); }
-        fs.partial_floats = floats;
-    }
-    if (counters > fs.ncounters) {
-        if (fs.counters) { (void)hipStreamSynchronize(ctx->stream); (void)hipFree(fs.counters); }
-        fs.counters = nullptr;
-        hipError_t e = hipMalloc(&fs.counters, counters * sizeof(int));
-        if (e == hipSuccess) e = hipMemset(fs.counters, 0, counters * sizeof(int));
-        if (e != hipSuccess) { fs.ncounters = 0; return hip_fail(ctx, e, "gemv_fast counters"); }
-        fs.ncounters = counters;
-    }
-    return TRHIP_OK;
 }
 
 template <int D>

@@ -138,15 +138,6 @@ __device__ __forceinline__ float exact_dot_row(const Planes p, int64_t row, cons
 
 }  // namespace trhip
 
-// Host-side objects.
-namespace trhip {
-struct FastScratch {  // partial sums and arrival counters of the split-K GEMV (gemv_fast.hip)
-    float *partials = nullptr;
-    size_t partial_floats = 0;
-    int *counters = nullptr;
-    size_t ncounters = 0;
-};
-}  // namespace trhip
 
 struct trhip_ctx {
     int device = 0;
@@ -156,7 +147,6 @@ struct trhip_ctx {
     void *ws = nullptr;
     size_t ws_bytes = 0;
     int sm_count = 0;
-    trhip::FastScratch fast;
 };
 
 struct trhip_wstore {
