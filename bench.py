@@ -59,9 +59,61 @@ def parse():
                     help="headline mode; the other mode is measured and reported beside it")
     ap.add_argument("--prefill-m", type=int, default=512)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample (0 = skip)")
+    ap.add_argument("--sweep", type=int, default=1, help="also time the 32-layer decode sweep (0 = skip)")
     ap.add_argument("--profile-kernel", choices=["gemv", "prefill", "copy"], default=None,
                     help="run only this kernel --steps times, eagerly (counter runs)")
     return ap.parse_args()
+
+
+LAYER = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
+         ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
+N_LAYERS, VOCAB, HIDDEN = 32, 128256, 4096
+
+
+def decode_sweep(tb, batches, mode, replays=5):
+    """One token step of a 32-layer Llama-3-8B-shaped model: every linear as a quantized GEMV (q4_k), back to
+    back, then the q6_k output head. Each layer owns its own device copy of the weights (4.36 GB in HBM), filled
+    with random-code blocks (synth.random_blocks): throughput does not depend on the values. Batch b > 1 runs
+    the M = b fp32 path. Timed as a captured graph replayed `replays` times."""
+    from tcb_amd import Q4K, Q6K, _lib, synth
+    L = _lib.lib()
+    ctx = tb.ctx
+    host = {name: synth.random_blocks(Q4K, n, k, seed=10 + i) for i, (name, n, k) in enumerate(LAYER)}
+    stores = [[tb.FromQuantized(Q4K, host[name], n, k) for name, n, k in LAYER] for _ in range(N_LAYERS)]
+    head = tb.FromQuantized(Q6K, synth.random_blocks(Q6K, VOCAB, HIDDEN, seed=99), VOCAB, HIDDEN)
+    del host
+    wbytes = sum(w.device_bytes() for layer in stores for w in layer) + head.device_bytes()
+    res = {}
+    for b in batches:
+        xs = {4096: ctx.to_device(synth.activations(b, 4096, seed=7)), 14336: ctx.to_device(synth.activations(b, 14336, seed=8))}
+        cb = ctx.alloc(b * VOCAB * 4)
+
+        def step():
+            for layer in stores:
+                for (name, n, k), w in zip(LAYER, layer):
+                    tb.GemmSet(b, n, k, xs[k], w, cb, mode=mode)
+            tb.GemmSet(b, VOCAB, HIDDEN, xs[4096], head, cb, mode=mode)
+
+        step()  # sizes the workspace
+        ctx.sync()
+        g = capture(tb, step)
+        time_graph(tb, g, 1)
+        ms = time_graph(tb, g, replays) / replays
+        L.trhip_graph_destroy(g)
+        res["batch%d" % b] = {"ms_per_token_step": round(ms, 4), "tokens_per_s": round(b / (ms * 1e-3), 1),
+                              "weight_GB/s": round(wbytes / (ms * 1e-3) / 1e9, 1),
+                              "hbm_frac_of_peak": round(wbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        for v in xs.values():
+            v.free()
+        cb.free()
+    for layer in stores:
+        for w in layer:
+            w.release()
+    head.release()
+    res.update({"workload": "32 layers x (q, k, v, o, gate, up, down) q4_k + q6_k head 128256x4096, %d GEMV launches "
+                            "per token step, weights %d B" % (7 * N_LAYERS + 1, wbytes),
+                "mode": "fast" if mode else "exact", "weight_bytes": wbytes})
+    return res
 
 
 def profile_kernel(a):
@@ -208,6 +260,8 @@ def main():
         Xb.free()
         Cb.free()
 
+    sweep = decode_sweep(tb, (1, 16), mode) if a.sweep else None
+
     # CPU baseline: AVX2 restatement of the reference's sdotq4k GEMV, all host cores, same bytes
     cpu = None
     if a.cpu_seconds > 0:
@@ -260,6 +314,7 @@ def main():
                      "frac": round(gbs_cold / HBM_PEAK_GBS, 4), "traffic": TRAFFIC.get(a.mode),
                      "kernel": "gemv_q4_k_%s" % a.mode, "algorithmic_bytes_per_launch": abytes},
         "prefill": prefill,
+        "decode_sweep": sweep,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

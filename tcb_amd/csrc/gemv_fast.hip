@@ -11,6 +11,7 @@
 // this path, gpu/kernel_quant_gemv.go:14-16). q4_k only; the other dtypes use the exact kernel.
 #include "trhip_internal.hpp"
 
+#include <cstdio>
 #include <cstdlib>
 
 namespace trhip {
@@ -31,26 +32,29 @@ __device__ __forceinline__ void fma_nib4(float &p, uint32_t nib4, float4 xv) {
 
 // Eight lanes per row; lane (g, h) = (lane8 >> 1, lane8 & 1) owns the 16 qs bytes 32g + 16h .. +16 of
 // every block: low nibbles are elements 16h..16h+15 of sub-block 2g, high nibbles the same elements of
-// sub-block 2g+1. A workgroup is 16 rows x 2 halves of K: wave w takes rows 8*(w>>1)..+8 and blocks of
-// half w&1. The halves meet in LDS (half 0 + half 1), then the 8 lanes of a row add with a fixed
-// xor-butterfly. x lives in LDS with a 16-byte pad per 256 bytes (the 8 slices a wave reads per step fall
-// in distinct banks), its 16-element sums next to it. Weights and x are both read one step ahead.
-template <bool ACC, int D>
-__global__ __launch_bounds__(256) void gemv_fast_q4k(const Planes p, const float *__restrict__ x,
-                                                     float *__restrict__ c, int64_t N, int64_t row0, int64_t K) {
+// sub-block 2g+1. A wave covers 8 rows. A workgroup is WAVES waves; with KS = 2 the waves pair up on the
+// same 8 rows and take one half of K each (the halves meet in LDS, half 0 + half 1), with KS = 1 each wave
+// owns its rows' whole K. The 8 lanes of a row then add with a fixed xor-butterfly. x lives in LDS with a
+// 16-byte pad per 256 bytes (the 8 slices a wave reads per step fall in distinct banks), its 16-element
+// sums next to it. Weights are requested D blocks ahead, x one block ahead.
+template <bool ACC, int D, int WAVES, int KS>
+__global__ __launch_bounds__(64 * WAVES) void gemv_fast_q4k(const Planes p, const float *__restrict__ x,
+                                                            float *__restrict__ c, int64_t N, int64_t row0, int64_t K) {
+    constexpr int THREADS = 64 * WAVES, ROWS = 8 * WAVES / KS;
     extern __shared__ float4 lds4[];
-    __shared__ float half_part[128];
+    __shared__ float half_part[KS == 2 ? 64 * WAVES / 2 : 1];
     const int nx4 = (int)(K / 4);
     float4 *xs = lds4;                                             // padded: nx4 + nx4/16 float4
     float *sx = reinterpret_cast<float *>(lds4 + nx4 + nx4 / 16);  // K/16 floats
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane8 = lane & 7, g = lane8 >> 1, hsel = lane8 & 1;
-    const int64_t r = (int64_t)blockIdx.x * 16 + 8 * (w >> 1) + (lane >> 3);
+    const int rg = w / KS, part = w % KS;
+    const int64_t r = (int64_t)blockIdx.x * ROWS + 8 * rg + (lane >> 3);
     const int64_t row = row0 + (r < N ? r : N - 1);
     const int nb = (int)p.nb;
     const int nh = (nb + 1) / 2;
-    const int b0 = (w & 1) ? nh : 0, b1 = (w & 1) ? nb : nh;
+    const int b0 = KS == 1 ? 0 : (part ? nh : 0), b1 = KS == 1 ? nb : (part ? nb : nh);
     const uint4 *hp = reinterpret_cast<const uint4 *>(p.aux) + row * nb;
     const uint4 *qp = reinterpret_cast<const uint4 *>(p.qs) + row * nb * 8 + 4 * hsel + g;
     uint4 H[D], Q[D];
@@ -61,7 +65,7 @@ __global__ __launch_bounds__(256) void gemv_fast_q4k(const Planes p, const float
         Q[s] = qp[8 * b];
     }
     const float4 *x4 = reinterpret_cast<const float4 *>(x);
-    for (int i = threadIdx.x; i < (int)(K / 16); i += 256) {
+    for (int i = threadIdx.x; i < (int)(K / 16); i += THREADS) {
         float4 a = x4[4 * i], b = x4[4 * i + 1], cc = x4[4 * i + 2], dd = x4[4 * i + 3];
         float4 *o = xs + 4 * i + (i >> 2);  // padded index of 4i: 4i + (4i >> 4)
         o[0] = a;
@@ -133,26 +137,29 @@ __global__ __launch_bounds__(256) void gemv_fast_q4k(const Planes p, const float
             }
         }
     }
-    if (w & 1) half_part[64 * (w >> 1) + lane] = acc;
-    __syncthreads();
-    if (w & 1) return;
-    acc = acc + half_part[64 * (w >> 1) + lane];
+    if (KS == 2) {
+        if (part) half_part[64 * rg + lane] = acc;
+        __syncthreads();
+        if (part) return;
+        acc = acc + half_part[64 * rg + lane];
+    }
     acc += __shfl_xor(acc, 1);
     acc += __shfl_xor(acc, 2);
     acc += __shfl_xor(acc, 4);
     if (lane8 == 0 && r < N) c[r] = ACC ? c[r] + acc : acc;
 }
 
-template <int D>
+template <int D, int WAVES, int KS>
 int run_q4k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c, bool acc) {
+    constexpr int ROWS = 8 * WAVES / KS;
     const int64_t nx4 = w->K / 4;
     size_t lds = (size_t)(nx4 + nx4 / 16) * sizeof(float4) + (size_t)(w->K / 16) * sizeof(float);
     if (lds > 150 * 1024) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv_fast: K too large for the LDS copy of x");
-    dim3 grid((unsigned)((N + 15) / 16)), block(256);
+    dim3 grid((unsigned)((N + ROWS - 1) / ROWS)), block(64 * WAVES);
     if (acc)
-        hipLaunchKernelGGL((gemv_fast_q4k<true, D>), grid, block, lds, ctx->stream, w->planes(), x, c, N, row0, w->K);
+        hipLaunchKernelGGL((gemv_fast_q4k<true, D, WAVES, KS>), grid, block, lds, ctx->stream, w->planes(), x, c, N, row0, w->K);
     else
-        hipLaunchKernelGGL((gemv_fast_q4k<false, D>), grid, block, lds, ctx->stream, w->planes(), x, c, N, row0, w->K);
+        hipLaunchKernelGGL((gemv_fast_q4k<false, D, WAVES, KS>), grid, block, lds, ctx->stream, w->planes(), x, c, N, row0, w->K);
     return launch_check(ctx, "gemv_fast_q4k");
 }
 
@@ -164,15 +171,32 @@ int launch_gemv(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, 
 int launch_gemv_fast(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                      bool acc) {
     if (w->dtype == kQ4K) {
-        // blocks in flight per lane: 2 measured fastest on the 14336x4096 cold ring; TRHIP_FAST_DEPTH (2, 4 or 8)
-        // overrides
-        static const int dep = [] {
-            const char *e = getenv("TRHIP_FAST_DEPTH");
-            return e ? atoi(e) : 2;
+        // launch shape "D,WAVES,KS": blocks in flight per lane, waves per workgroup, K parts per row group.
+        // Measured on cold 1.1 GiB rings at K = 4096: splitting K in two wins while the grid is small (1024 and
+        // 4096 rows: 5.5 / 5.9 us vs 7.9 / 8.2), whole rows per wave win from ~8192 rows up (14336 rows:
+        // 10.65 us vs 11.7). TRHIP_FAST_CFG overrides.
+        static const int forced = [] {
+            const char *e = getenv("TRHIP_FAST_CFG");
+            int d = 0, wv = 0, ks = 0;
+            if (e && sscanf(e, "%d,%d,%d", &d, &wv, &ks) == 3) return 100 * d + 10 * wv + ks;
+            return 0;
         }();
-        if (dep == 2) return run_q4k<2>(ctx, w, row0, N, x, c, acc);
-        if (dep == 8) return run_q4k<8>(ctx, w, row0, N, x, c, acc);
-        return run_q4k<4>(ctx, w, row0, N, x, c, acc);
+        const int cfg = forced ? forced : (N >= 8192 ? 241 : 242);
+        switch (cfg) {
+        case 242: return run_q4k<2, 4, 2>(ctx, w, row0, N, x, c, acc);
+        case 442: return run_q4k<4, 4, 2>(ctx, w, row0, N, x, c, acc);
+        case 241: return run_q4k<2, 4, 1>(ctx, w, row0, N, x, c, acc);
+        case 441: return run_q4k<4, 4, 1>(ctx, w, row0, N, x, c, acc);
+        case 841: return run_q4k<8, 4, 1>(ctx, w, row0, N, x, c, acc);
+        case 421: return run_q4k<4, 2, 1>(ctx, w, row0, N, x, c, acc);
+        case 221: return run_q4k<2, 2, 1>(ctx, w, row0, N, x, c, acc);
+        case 282: return run_q4k<2, 8, 2>(ctx, w, row0, N, x, c, acc);
+        case 482: return run_q4k<4, 8, 2>(ctx, w, row0, N, x, c, acc);
+        case 481: return run_q4k<4, 8, 1>(ctx, w, row0, N, x, c, acc);
+        case 411: return run_q4k<4, 1, 1>(ctx, w, row0, N, x, c, acc);
+        case 811: return run_q4k<8, 1, 1>(ctx, w, row0, N, x, c, acc);
+        }
+        return run_q4k<2, 4, 2>(ctx, w, row0, N, x, c, acc);
     }
     return launch_gemv(ctx, w, row0, N, x, c, acc, TRHIP_MODE_EXACT);
 }

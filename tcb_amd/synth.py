@@ -178,3 +178,26 @@ def quant_weights(dt, N, K, seed, std=0.02, outliers=0.0, chunk_rows=128):
 
 def activations(M, K, seed):
     return normal(M * K, seed).reshape(M, K)
+
+
+def random_blocks(dt, N, K, seed):
+    """Blocks of uniformly random codes with moderate fp16 scales (d ~ 2^-7, q4_k dmin ~ 2^-8, q6_k signed
+    scales kept): well-formed inputs for throughput runs over many large tensors, where encoding real weights
+    would dominate the run time. Values are not meant to look like trained weights."""
+    bb = {Q8: 34, Q4: 18, Q4K: 144, Q6K: 210}[dt]
+    be = 32 if dt in (Q8, Q4) else 256
+    nb = N * (K // be)
+    rng = np.random.default_rng(seed)
+    # at most 2^16 distinct random blocks, repeated: generating hundreds of MB of random bytes costs seconds
+    uniq = min(nb, 1 << 16)
+    base = np.frombuffer(rng.bytes(uniq * bb), dtype=np.uint8).reshape(uniq, bb)
+    raw = np.resize(base, (nb, bb))
+    d = _f16_bits(np.full(1, 2.0 ** -7, np.float32)).view(np.uint8)
+    if dt in (Q8, Q4):
+        raw[:, 0:2] = d
+    elif dt == Q4K:
+        raw[:, 0:2] = d
+        raw[:, 2:4] = _f16_bits(np.full(1, 2.0 ** -8, np.float32)).view(np.uint8)
+    else:
+        raw[:, 208:210] = d
+    return raw.reshape(-1)
