@@ -20,6 +20,8 @@
 // 8(v/4)+4(l/32)+v%4, column l%32) were checked on the device against host matrix products.
 #include "trhip_internal.hpp"
 
+#include <cstdlib>
+
 namespace trhip {
 namespace {
 
@@ -29,11 +31,17 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 
-constexpr int TM = 64, TN = 128, THREADS = 256, MT = TM / 32;
-constexpr int ABYTES = TM * 256;  // activation codes of one block, in MFMA lane order
-constexpr int SBYTES = TM * 32;   // f16 msum operand of one block, in MFMA lane order
-constexpr int STAGE = ABYTES + SBYTES + TM * sizeof(float);
-constexpr size_t kLds = 2 * STAGE + (TM + 1) * sizeof(int);
+constexpr int TN = 128, THREADS = 256;
+// Per row-tile height TM (64 or 32): LDS staging of one block, in MFMA lane order.
+template <int TM>
+struct Tile {
+    static constexpr int MT = TM / 32;           // 32-row MFMA tiles per wave
+    static constexpr int ABYTES = TM * 256;      // activation codes of one block
+    static constexpr int SBYTES = TM * 32;       // f16 msum operand of one block
+    static constexpr int STAGE = ABYTES + SBYTES + TM * (int)sizeof(float);
+    static constexpr size_t LDS = 2 * STAGE + (TM + 1) * sizeof(int);
+    static constexpr int CPW = TM / 16;          // 1 KB activation chunks staged per wave (THREADS = 256)
+};
 
 // Four bytes (each < 16) times s (< 8) with one packed 16-bit multiply: the products (< 128) stay in
 // their bytes, so nothing carries into the neighbour.
@@ -64,11 +72,13 @@ __device__ __forceinline__ void tile_of(int64_t wg, int64_t mt, int64_t nt, int6
 
 // msum = sum_j S_j m_j with S_j = 64 Sh_j + Sl_j: one f16 MFMA over k = [Sh_0..7 | Sl_0..7] x [64 m_0..7 | m_0..7].
 // Every product and partial sum is an integer below 2^24, so the fp32 result is msum exactly.
-template <bool ACC>
-__global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void actq_mfma_q4k(
+template <bool ACC, int TM>
+__global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(TM == 64 ? 2 : 3, TM == 64 ? 2 : 4))) void actq_mfma_q4k(
     const Planes p, int64_t N, int64_t row0, int64_t M, int64_t K, const float *__restrict__ x,
     const int8_t *__restrict__ q, const float *__restrict__ d8, const uint16_t *__restrict__ sj,
     const uint8_t *__restrict__ bad_blk, float *__restrict__ c) {
+    using T = Tile<TM>;
+    constexpr int MT = T::MT, ABYTES = T::ABYTES, SBYTES = T::SBYTES, STAGE = T::STAGE, CPW = T::CPW;
     extern __shared__ __align__(16) uint8_t lds[];
     int *rowstate = reinterpret_cast<int *>(lds + 2 * STAGE);  // [TM] 0 ok, 1 NaN/Inf row, 2 outside M
     int *anybad = rowstate + TM;                                // some row of the tile is 1
@@ -93,29 +103,31 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
         rowstate[i] = st;
     }
 
-    // activation staging: thread tid owns lane tid & 63 of tile t4 = (tid >> 6) & 1 (rows 32 t4 .. +31), chunks
-    // kc = 4 (tid >> 7) .. +3; threads < 128 also stage the msum operand of tile t4, threads < TM one scale each
-    const int t4 = (tid >> 6) & 1, kc0 = 4 * (tid >> 7);
+    // activation staging: wave w stages chunks c = CPW w .. +CPW-1 (tile c / 8, kc c % 8), lane tid & 63 of each;
+    // threads < 2 TM also stage the msum operand (tile tid >> 6), threads < TM one scale each
+    const int c0i = CPW * w, t4 = c0i >> 3, kc0 = c0i & 7;
     const int64_t sm0 = m0 + 32 * t4 + (lane & 31);
     const int64_t sm = sm0 < M ? sm0 : M - 1;
     const v4i *ag = reinterpret_cast<const v4i *>(q + sm * K) + (lane >> 5) + 2 * kc0;  // + 16 b + 2 r
-    const v4i *sg = reinterpret_cast<const v4i *>(sj + sm * nb * 16) + (lane >> 5);  // + 2 b
+    const int64_t ss0 = m0 + 32 * (tid >> 6) + (lane & 31);  // msum operand row (threads < 2 TM)
+    const int64_t srow = ss0 < M ? ss0 : M - 1;
+    const v4i *sg2 = reinterpret_cast<const v4i *>(sj + srow * nb * 16) + (lane >> 5);  // + 2 b
     const int64_t dm0 = m0 + (tid & (TM - 1));
     const float *dg = d8 + (dm0 < M ? dm0 : M - 1) * nb;
-    v4i sa[4], ss = (v4i){0};
+    v4i sa[CPW], ss = (v4i){0};
     float sd8 = 0.0f;
     auto fetch_a = [&](int b) {
 #pragma unroll
-        for (int r = 0; r < 4; r++) sa[r] = ag[16 * b + 2 * r];
-        if (tid < 128) ss = sg[2 * b];
+        for (int r = 0; r < CPW; r++) sa[r] = ag[16 * b + 2 * r];
+        if (tid < 2 * TM) ss = sg2[2 * b];
         if (tid < TM) sd8 = dg[b];
     };
     auto put_a = [&](int buf) {
         uint8_t *st = lds + buf * STAGE;
         v4i *ad = reinterpret_cast<v4i *>(st + (8 * t4 + kc0) * 1024) + lane;
 #pragma unroll
-        for (int r = 0; r < 4; r++) ad[64 * r] = sa[r];
-        if (tid < 128) reinterpret_cast<v4i *>(st + ABYTES)[tid] = ss;
+        for (int r = 0; r < CPW; r++) ad[64 * r] = sa[r];
+        if (tid < 2 * TM) reinterpret_cast<v4i *>(st + ABYTES)[tid] = ss;
         if (tid < TM) reinterpret_cast<float *>(st + ABYTES + SBYTES)[tid] = sd8;
     };
 
@@ -236,27 +248,43 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
     }
 }
 
-}  // namespace
 
-int launch_actq_mfma(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
-                     int64_t M, bool acc, const int8_t *q, const float *d, const uint16_t *sj, const uint8_t *bad) {
-    if (w->dtype != kQ4K) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "actq_mfma: q4_k only");
+template <int TM>
+int run_mfma(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c, int64_t M,
+             bool acc, const int8_t *q, const float *d, const uint16_t *sj, const uint8_t *bad) {
+    constexpr size_t lds = Tile<TM>::LDS;
     dim3 grid((unsigned)(((N + TN - 1) / TN) * ((M + TM - 1) / TM))), block(THREADS);
     static bool lds_set = false;  // more than 64 KB of dynamic LDS has to be allowed once per kernel
     if (!lds_set) {
-        hipError_t e1 = hipFuncSetAttribute(reinterpret_cast<const void *>(&actq_mfma_q4k<true>),
-                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLds);
-        hipError_t e2 = hipFuncSetAttribute(reinterpret_cast<const void *>(&actq_mfma_q4k<false>),
-                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLds);
+        hipError_t e1 = hipFuncSetAttribute(reinterpret_cast<const void *>(&actq_mfma_q4k<true, TM>),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        hipError_t e2 = hipFuncSetAttribute(reinterpret_cast<const void *>(&actq_mfma_q4k<false, TM>),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e1 != hipSuccess) return hip_fail(ctx, e1, "actq_mfma: LDS size");
         if (e2 != hipSuccess) return hip_fail(ctx, e2, "actq_mfma: LDS size");
         lds_set = true;
     }
     if (acc)
-        hipLaunchKernelGGL(actq_mfma_q4k<true>, grid, block, kLds, ctx->stream, w->planes(), N, row0, M, w->K, x, q, d, sj, bad, c);
+        hipLaunchKernelGGL((actq_mfma_q4k<true, TM>), grid, block, lds, ctx->stream, w->planes(), N, row0, M, w->K, x, q, d,
+                           sj, bad, c);
     else
-        hipLaunchKernelGGL(actq_mfma_q4k<false>, grid, block, kLds, ctx->stream, w->planes(), N, row0, M, w->K, x, q, d, sj, bad, c);
+        hipLaunchKernelGGL((actq_mfma_q4k<false, TM>), grid, block, lds, ctx->stream, w->planes(), N, row0, M, w->K, x, q,
+                           d, sj, bad, c);
     return launch_check(ctx, "actq_mfma_q4k");
+}
+
+}  // namespace
+
+int launch_actq_mfma(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
+                     int64_t M, bool acc, const int8_t *q, const float *d, const uint16_t *sj, const uint8_t *bad) {
+    if (w->dtype != kQ4K) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "actq_mfma: q4_k only");
+    // row-tile height: TRHIP_ACTQ_TM (32 or 64) overrides the default
+    static const int tm = [] {
+        const char *e = getenv("TRHIP_ACTQ_TM");
+        return (e && atoi(e) == 32) ? 32 : 64;
+    }();
+    if (tm == 32) return run_mfma<32>(ctx, w, row0, N, x, c, M, acc, q, d, sj, bad);
+    return run_mfma<64>(ctx, w, row0, N, x, c, M, acc, q, d, sj, bad);
 }
 
 }  // namespace trhip

@@ -236,6 +236,179 @@ __global__ __launch_bounds__(THREADS) void gemv_exact_kernel(const Planes p, con
     }
 }
 
+// ---------------------------------------------------------------- eight lanes per row
+// The same arithmetic with twice the lanes per row: lane u (0..7) owns the four chains 4u..4u+3 (half u&1 of
+// sdot32 register u>>1), i.e. elements 32G + 4u .. +3 of every 32-element group G in ascending G. Each lane
+// reads aligned 4-byte pieces of the same plane layout. The tree: (A0+A1) and (A2+A3) by xor-shuffle 2, their
+// sum by xor 4, s_l = Y[l] + Y[l+4] by xor 1, then (s0+s2)+(s1+s3) in-lane; IEEE addition is commutative, so
+// the partners of every shuffle hold identical bits.
+template <int DT>
+struct Blk8;
+
+template <>
+struct Blk8<kQ8> {
+    static constexpr int DEPTH = 24;
+    struct Data { uint32_t q, d; };
+    const uint32_t *qp;
+    const uint16_t *dp;
+    __device__ Blk8(const Planes &p, int64_t row, int u)
+        : qp(reinterpret_cast<const uint32_t *>(p.qs + row * p.nb * 32) + u), dp(p.d + row * p.nb) {}
+    __device__ __forceinline__ void load(Data &v, int64_t b) const { v.q = qp[8 * b]; v.d = dp[b]; }
+    __device__ __forceinline__ void compute(float *acc, const Data &v, const float4 *xb) const {
+        const float d = f16_to_f32((uint16_t)v.d);
+        fma4(acc, v.q ^ 0x80808080u, d, -128.0f * d, xb[0]);  // (u - 128)*d exact
+    }
+    static constexpr int XSTEP = 8;  // float4s of x per block
+};
+
+template <>
+struct Blk8<kQ4> {
+    static constexpr int DEPTH = 24;
+    struct Data { uint32_t q, d; };
+    const uint32_t *qp;
+    const uint16_t *dp;
+    int sh;
+    __device__ Blk8(const Planes &p, int64_t row, int u)
+        : qp(reinterpret_cast<const uint32_t *>(p.qs + row * p.nb * 16) + (u & 3)), dp(p.d + row * p.nb),
+          sh(u >= 4 ? 4 : 0) {}  // lanes 4..7 take the high nibbles (elements 16..31)
+    __device__ __forceinline__ void load(Data &v, int64_t b) const { v.q = qp[4 * b]; v.d = dp[b]; }
+    __device__ __forceinline__ void compute(float *acc, const Data &v, const float4 *xb) const {
+        const float d = f16_to_f32((uint16_t)v.d);
+        fma4(acc, (v.q >> sh) & 0x0F0F0F0Fu, d, -8.0f * d, xb[0]);
+    }
+    static constexpr int XSTEP = 8;
+};
+
+template <>
+struct Blk8<kQ4K> {
+    static constexpr int DEPTH = 6;
+    struct Data { uint4 h; uint32_t q[4]; };
+    const uint4 *hp;
+    const uint32_t *qp;  // lane u's 4 bytes of group pair g: 64(u>>2) + 16g + 8((u>>1)&1) + 4(u&1)
+    __device__ Blk8(const Planes &p, int64_t row, int u)
+        : hp(reinterpret_cast<const uint4 *>(p.aux + row * p.nb * 16)),
+          qp(reinterpret_cast<const uint32_t *>(p.qs + row * p.nb * 128) + 16 * (u >> 2) + 2 * ((u >> 1) & 1) + (u & 1)) {}
+    __device__ __forceinline__ void load(Data &v, int64_t b) const {
+        v.h = hp[b];
+#pragma unroll
+        for (int g = 0; g < 4; g++) v.q[g] = qp[32 * b + 4 * g];
+    }
+    __device__ __forceinline__ void compute(float *acc, const Data &v, const float4 *xb) const {
+        const float d = f16_to_f32((uint16_t)(v.h.x & 0xFFFF)), dmin = f16_to_f32((uint16_t)(v.h.x >> 16));
+        const float d16 = d * 0.0625f;
+        uint32_t sc_lo, sc_hi, m_lo, m_hi;
+        q4k_scales(v.h.y, v.h.z, v.h.w, sc_lo, sc_hi, m_lo, m_hi);
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const uint32_t scw = g < 2 ? sc_lo : sc_hi, mw = g < 2 ? m_lo : m_hi;
+            const int k0 = (2 * g) & 3, k1 = (2 * g + 1) & 3;
+            const float s0 = d * ubyte_f(scw, k0), n0 = -(dmin * ubyte_f(mw, k0));
+            const float s1 = d16 * ubyte_f(scw, k1), n1 = -(dmin * ubyte_f(mw, k1));
+            // sub-block 2g: low nibbles; sub-block 2g+1: high nibbles read as 16*code with scale d/16 (exact)
+            fma4(acc, v.q[g] & 0x0F0F0F0Fu, s0, n0, xb[8 * (2 * g)]);
+            fma4(acc, v.q[g] & 0xF0F0F0F0u, s1, n1, xb[8 * (2 * g + 1)]);
+        }
+    }
+    static constexpr int XSTEP = 64;
+};
+
+template <>
+struct Blk8<kQ6K> {
+    static constexpr int DEPTH = 4;
+    struct Data { uint32_t l[4], hq[2]; uint4 sv; uint32_t d; };
+    const uint32_t *lp, *hp;
+    const uint4 *sp;
+    const uint16_t *dp;
+    int th;
+    __device__ Blk8(const Planes &p, int64_t row, int u)
+        : lp(reinterpret_cast<const uint32_t *>(p.qs + row * p.nb * 128) + 8 * (u >> 1) + (u & 1)),
+          hp(reinterpret_cast<const uint32_t *>(p.aux + row * p.nb * 64) + 4 * (u >> 1) + (u & 1)),
+          sp(reinterpret_cast<const uint4 *>(p.sc + row * p.nb * 16)), dp(p.d + row * p.nb), th(u >> 2) {}
+    __device__ __forceinline__ void load(Data &v, int64_t b) const {
+#pragma unroll
+        for (int i = 0; i < 4; i++) v.l[i] = lp[32 * b + 2 * i];  // ql bytes 32(u>>1) + 16n + 8h + 4(u&1), i = 2n + h
+#pragma unroll
+        for (int n = 0; n < 2; n++) v.hq[n] = hp[16 * b + 2 * n];  // qh bytes 16(u>>1) + 8n + 4(u&1)
+        v.sv = sp[b];
+        v.d = dp[b];
+    }
+    __device__ __forceinline__ void compute(float *acc, const Data &v, const float4 *xb) const {
+        const float d = f16_to_f32((uint16_t)v.d);
+        const uint32_t scw[4] = {v.sv.x, v.sv.y, v.sv.z, v.sv.w};
+#pragma unroll
+        for (int n = 0; n < 2; n++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t A = v.l[2 * n + (k & 1)];
+                const uint32_t nib = (k < 2) ? (A & 0x0F0F0F0Fu) : ((A >> 4) & 0x0F0F0F0Fu);
+                const uint32_t code = nib | (((v.hq[n] >> (2 * k)) & 0x03030303u) << 4);
+                const int si = 8 * n + 2 * k + th;  // 16-element scale of elements 4u..4u+3 of group 4n + k
+                const int8_t scv = (int8_t)((scw[si >> 2] >> (8 * (si & 3))) & 0xFF);
+                const float ds = d * (float)scv;  // exact (11 x 8 bits)
+                // fl(ds*(code-32)) == fmaf(ds, code, -32*ds): same real number, one rounding
+                fma4(acc, code, ds, -32.0f * ds, xb[8 * (4 * n + k)]);
+            }
+    }
+    static constexpr int XSTEP = 64;
+};
+
+__device__ __forceinline__ float sdot32_tree8(const float *acc) {
+    float s[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float p = acc[i] + __shfl_xor(acc[i], 2);  // A0+A1 (lanes 0-3), A2+A3 (lanes 4-7)
+        const float y = p + __shfl_xor(p, 4);            // Y[4(u&1) + i]
+        s[i] = y + __shfl_xor(y, 1);                     // s_i = Y[i] + Y[i+4]
+    }
+    return (s[0] + s[2]) + (s[1] + s[3]);
+}
+
+template <int DT, bool ACC, int THREADS>
+__global__ __launch_bounds__(THREADS) void gemv_exact8_kernel(const Planes p, const float *__restrict__ x,
+                                                              float *__restrict__ c, int64_t N, int64_t row0, int64_t K) {
+    extern __shared__ float4 xs[];  // K / 4 float4: the whole activation vector
+    const int u = threadIdx.x & 7;
+    const int64_t r = (int64_t)blockIdx.x * (THREADS / 8) + (threadIdx.x >> 3);
+    const bool live = r < N;
+    const int64_t row = row0 + (live ? r : 0);
+    const int64_t nb = p.nb;
+    using B = Blk8<DT>;
+    constexpr int D = B::DEPTH;
+    B blk(p, row, u);
+    typename B::Data ring[D];
+#pragma unroll
+    for (int s = 0; s < D; s++) blk.load(ring[s], s < nb ? s : nb - 1);
+    stage_x<THREADS>(xs, reinterpret_cast<const float4 *>(x), K / 4);
+    __syncthreads();
+
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const float4 *xl = xs + u;
+    for (int64_t b0 = 0; b0 < nb; b0 += D) {
+#pragma unroll
+        for (int s = 0; s < D; s++) {
+            const int64_t b = b0 + s;
+            typename B::Data cur = ring[s];
+            blk.load(ring[s], (b + D < nb) ? b + D : nb - 1);
+            if (b < nb) blk.compute(acc, cur, xl + B::XSTEP * b);
+        }
+    }
+    const float res = sdot32_tree8(acc);
+    if (live && u == 0) {
+        if (ACC) c[r] = c[r] + res;
+        else c[r] = res;
+    }
+}
+
+template <int DT, int THREADS>
+void launch_exact8_t(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
+                     bool acc, size_t lds) {
+    dim3 grid((unsigned)((N + THREADS / 8 - 1) / (THREADS / 8))), block(THREADS);
+    if (acc)
+        hipLaunchKernelGGL((gemv_exact8_kernel<DT, true, THREADS>), grid, block, lds, ctx->stream, w->planes(), x, c, N, row0, w->K);
+    else
+        hipLaunchKernelGGL((gemv_exact8_kernel<DT, false, THREADS>), grid, block, lds, ctx->stream, w->planes(), x, c, N, row0, w->K);
+}
+
 template <int DT, int THREADS>
 void launch_exact_t(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                     bool acc, size_t lds) {
@@ -265,6 +438,21 @@ int launch_exact(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N,
                  bool acc) {
     size_t lds = (size_t)w->K * sizeof(float);
     if (lds > 160 * 1024) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv: K too large for the LDS copy of x");
+    // lanes per row: 8 measured faster for q4_k (14336x4096 cold: 15.7 vs 18.0 us; 1024x4096: 12.5 vs 15.9),
+    // q8_0 (4096x4096: 20.3 vs 23.6) and equal for q4_0; 4 stays faster for q6_k (128256x4096: 109 vs 139 us).
+    // TRHIP_EXACT_LANES (4 or 8) overrides.
+    static const int forced = [] {
+        const char *e = getenv("TRHIP_EXACT_LANES");
+        const int v = e ? atoi(e) : 0;
+        return (v == 4 || v == 8) ? v : 0;
+    }();
+    const int lanes = forced ? forced : (DT == kQ6K ? 4 : 8);
+    if (lanes == 8) {
+        // 8 lanes per row: 32 rows per 256-thread workgroup, 16 per 128-thread one for small N
+        if (N >= 32 * 200) launch_exact8_t<DT, 256>(ctx, w, row0, N, x, c, acc, lds);
+        else launch_exact8_t<DT, 128>(ctx, w, row0, N, x, c, acc, lds);
+        return launch_check(ctx, "gemv_exact8");
+    }
     switch (gemv_rows_per_wg(N)) {
     case 64: launch_exact_t<DT, 256>(ctx, w, row0, N, x, c, acc, lds); break;
     case 32: launch_exact_t<DT, 128>(ctx, w, row0, N, x, c, acc, lds); break;

@@ -32,17 +32,19 @@ __device__ __forceinline__ void fma_nib4(float &p, uint32_t nib4, float4 xv) {
 
 // Eight lanes per row; lane (g, h) = (lane8 >> 1, lane8 & 1) owns the 16 qs bytes 32g + 16h .. +16 of
 // every block: low nibbles are elements 16h..16h+15 of sub-block 2g, high nibbles the same elements of
-// sub-block 2g+1. A wave covers 8 rows. A workgroup is WAVES waves; with KS = 2 the waves pair up on the
-// same 8 rows and take one half of K each (the halves meet in LDS, half 0 + half 1), with KS = 1 each wave
-// owns its rows' whole K. The 8 lanes of a row then add with a fixed xor-butterfly. x lives in LDS with a
-// 16-byte pad per 256 bytes (the 8 slices a wave reads per step fall in distinct banks), its 16-element
-// sums next to it. Weights are requested D blocks ahead, x one block ahead.
-template <bool ACC, int D, int WAVES, int KS>
+// sub-block 2g+1. Each lane serves R rows (8 apart) with the same x, so a wave covers 8R rows and every x
+// slice read from LDS feeds R rows (LDS read bandwidth, not HBM, bounds this kernel at R = 1). A workgroup is
+// WAVES waves; with KS = 2 the waves pair up on the same rows and take one half of K each (the halves meet in
+// LDS, half 0 + half 1), with KS = 1 each wave owns its rows' whole K. The 8 lanes of a row then add with a
+// fixed xor-butterfly. x lives in LDS with a 16-byte pad per 256 bytes (the 8 slices a wave reads per step
+// fall in distinct banks), its 16-element sums next to it. Weights are requested D blocks ahead, x one block
+// ahead.
+template <bool ACC, int D, int WAVES, int KS, int R>
 __global__ __launch_bounds__(64 * WAVES) void gemv_fast_q4k(const Planes p, const float *__restrict__ x,
                                                             float *__restrict__ c, int64_t N, int64_t row0, int64_t K) {
-    constexpr int THREADS = 64 * WAVES, ROWS = 8 * WAVES / KS;
+    constexpr int THREADS = 64 * WAVES, ROWS = 8 * R * WAVES / KS;
     extern __shared__ float4 lds4[];
-    __shared__ float half_part[KS == 2 ? 64 * WAVES / 2 : 1];
+    __shared__ float half_part[KS == 2 ? 64 * R * WAVES / 2 : 1];
     const int nx4 = (int)(K / 4);
     float4 *xs = lds4;                                             // padded: nx4 + nx4/16 float4
     float *sx = reinterpret_cast<float *>(lds4 + nx4 + nx4 / 16);  // K/16 floats
@@ -50,19 +52,27 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_fast_q4k(const Planes p, cons
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane8 = lane & 7, g = lane8 >> 1, hsel = lane8 & 1;
     const int rg = w / KS, part = w % KS;
-    const int64_t r = (int64_t)blockIdx.x * ROWS + 8 * rg + (lane >> 3);
-    const int64_t row = row0 + (r < N ? r : N - 1);
     const int nb = (int)p.nb;
     const int nh = (nb + 1) / 2;
     const int b0 = KS == 1 ? 0 : (part ? nh : 0), b1 = KS == 1 ? nb : (part ? nb : nh);
-    const uint4 *hp = reinterpret_cast<const uint4 *>(p.aux) + row * nb;
-    const uint4 *qp = reinterpret_cast<const uint4 *>(p.qs) + row * nb * 8 + 4 * hsel + g;
-    uint4 H[D], Q[D];
+    int64_t r[R];
+    const uint4 *hp[R], *qp[R];
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+        r[i] = (int64_t)blockIdx.x * ROWS + 8 * R * rg + 8 * i + (lane >> 3);
+        const int64_t row = row0 + (r[i] < N ? r[i] : N - 1);
+        hp[i] = reinterpret_cast<const uint4 *>(p.aux) + row * nb;
+        qp[i] = reinterpret_cast<const uint4 *>(p.qs) + row * nb * 8 + 4 * hsel + g;
+    }
+    uint4 H[D][R], Q[D][R];
 #pragma unroll
     for (int s = 0; s < D; s++) {  // weights first: they come from HBM
         int b = b0 + s < b1 ? b0 + s : (b1 > b0 ? b1 - 1 : 0);
-        H[s] = hp[b];
-        Q[s] = qp[8 * b];
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            H[s][i] = hp[i][b];
+            Q[s][i] = qp[i][8 * b];
+        }
     }
     const float4 *x4 = reinterpret_cast<const float4 *>(x);
     for (int i = threadIdx.x; i < (int)(K / 16); i += THREADS) {
@@ -90,15 +100,22 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_fast_q4k(const Planes p, cons
             XH[cc] = xb[8 + cc];
         }
     }
-    float acc = 0.0f;
+    float acc[R];
+#pragma unroll
+    for (int i = 0; i < R; i++) acc[i] = 0.0f;
     for (int bb = b0; bb < b1; bb += D) {
 #pragma unroll
         for (int s = 0; s < D; s++) {
             const int b = bb + s;
-            const uint4 h = H[s], q = Q[s];
+            uint4 h[R], q[R];
             const int nx = b + D < b1 ? b + D : b1 - 1;
-            H[s] = hp[nx];
-            Q[s] = qp[8 * nx];
+#pragma unroll
+            for (int i = 0; i < R; i++) {
+                h[i] = H[s][i];
+                q[i] = Q[s][i];
+                H[s][i] = hp[i][nx];
+                Q[s][i] = qp[i][8 * nx];
+            }
             const float4 *xn = xg + 68 * (b + 1 < b1 ? b + 1 : b);
             float4 NL[4], NH[4];
 #pragma unroll
@@ -107,28 +124,32 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_fast_q4k(const Planes p, cons
                 NH[cc] = xn[8 + cc];
             }
             if (b < b1) {  // wave-uniform
-                float d = f16_to_f32((uint16_t)(h.x & 0xFFFF)), dmin = f16_to_f32((uint16_t)(h.x >> 16));
-                uint32_t sc_lo, sc_hi, m_lo, m_hi;
-                q4k_scales(h.y, h.z, h.w, sc_lo, sc_hi, m_lo, m_hi);
-                const uint32_t scw = g < 2 ? sc_lo : sc_hi, mw = g < 2 ? m_lo : m_hi;
-                const float d9 = d * 512.0f;  // undoes the 2^-9 of the fp8 reading
-                const float s0 = d9 * ubyte_f(scw, k0), n0 = -(dmin * ubyte_f(mw, k0));
-                const float s1 = d9 * ubyte_f(scw, k1), n1 = -(dmin * ubyte_f(mw, k1));
-                const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-                float pl0 = 0.0f, pl1 = 0.0f, ph0 = 0.0f, ph1 = 0.0f;
-#pragma unroll
-                for (int cc = 0; cc < 4; cc++) {
-                    const uint32_t lo = qw[cc] & 0x0F0F0F0Fu, hi = (qw[cc] >> 4) & 0x0F0F0F0Fu;
-                    float &pl = (cc & 1) ? pl1 : pl0;
-                    float &ph = (cc & 1) ? ph1 : ph0;
-                    fma_nib4(pl, lo, XL[cc]);
-                    fma_nib4(ph, hi, XH[cc]);
-                }
                 const float *sxb = sxg + 16 * b;
-                acc = fmaf(s0, pl0 + pl1, acc);
-                acc = fmaf(n0, sxb[0], acc);
-                acc = fmaf(s1, ph0 + ph1, acc);
-                acc = fmaf(n1, sxb[2], acc);
+                const float sl = sxb[0], shx = sxb[2];
+#pragma unroll
+                for (int i = 0; i < R; i++) {
+                    float d = f16_to_f32((uint16_t)(h[i].x & 0xFFFF)), dmin = f16_to_f32((uint16_t)(h[i].x >> 16));
+                    uint32_t sc_lo, sc_hi, m_lo, m_hi;
+                    q4k_scales(h[i].y, h[i].z, h[i].w, sc_lo, sc_hi, m_lo, m_hi);
+                    const uint32_t scw = g < 2 ? sc_lo : sc_hi, mw = g < 2 ? m_lo : m_hi;
+                    const float d9 = d * 512.0f;  // undoes the 2^-9 of the fp8 reading
+                    const float s0 = d9 * ubyte_f(scw, k0), n0 = -(dmin * ubyte_f(mw, k0));
+                    const float s1 = d9 * ubyte_f(scw, k1), n1 = -(dmin * ubyte_f(mw, k1));
+                    const uint32_t qw[4] = {q[i].x, q[i].y, q[i].z, q[i].w};
+                    float pl0 = 0.0f, pl1 = 0.0f, ph0 = 0.0f, ph1 = 0.0f;
+#pragma unroll
+                    for (int cc = 0; cc < 4; cc++) {
+                        const uint32_t lo = qw[cc] & 0x0F0F0F0Fu, hi = (qw[cc] >> 4) & 0x0F0F0F0Fu;
+                        float &pl = (cc & 1) ? pl1 : pl0;
+                        float &ph = (cc & 1) ? ph1 : ph0;
+                        fma_nib4(pl, lo, XL[cc]);
+                        fma_nib4(ph, hi, XH[cc]);
+                    }
+                    acc[i] = fmaf(s0, pl0 + pl1, acc[i]);
+                    acc[i] = fmaf(n0, sl, acc[i]);
+                    acc[i] = fmaf(s1, ph0 + ph1, acc[i]);
+                    acc[i] = fmaf(n1, shx, acc[i]);
+                }
             }
 #pragma unroll
             for (int cc = 0; cc < 4; cc++) {
@@ -138,28 +159,36 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_fast_q4k(const Planes p, cons
         }
     }
     if (KS == 2) {
-        if (part) half_part[64 * rg + lane] = acc;
+        if (part) {
+#pragma unroll
+            for (int i = 0; i < R; i++) half_part[64 * (R * rg + i) + lane] = acc[i];
+        }
         __syncthreads();
         if (part) return;
-        acc = acc + half_part[64 * rg + lane];
+#pragma unroll
+        for (int i = 0; i < R; i++) acc[i] = acc[i] + half_part[64 * (R * rg + i) + lane];
     }
-    acc += __shfl_xor(acc, 1);
-    acc += __shfl_xor(acc, 2);
-    acc += __shfl_xor(acc, 4);
-    if (lane8 == 0 && r < N) c[r] = ACC ? c[r] + acc : acc;
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+        float a = acc[i];
+        a += __shfl_xor(a, 1);
+        a += __shfl_xor(a, 2);
+        a += __shfl_xor(a, 4);
+        if (lane8 == 0 && r[i] < N) c[r[i]] = ACC ? c[r[i]] + a : a;
+    }
 }
 
-template <int D, int WAVES, int KS>
+template <int D, int WAVES, int KS, int R>
 int run_q4k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c, bool acc) {
-    constexpr int ROWS = 8 * WAVES / KS;
+    constexpr int ROWS = 8 * R * WAVES / KS;
     const int64_t nx4 = w->K / 4;
     size_t lds = (size_t)(nx4 + nx4 / 16) * sizeof(float4) + (size_t)(w->K / 16) * sizeof(float);
     if (lds > 150 * 1024) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv_fast: K too large for the LDS copy of x");
     dim3 grid((unsigned)((N + ROWS - 1) / ROWS)), block(64 * WAVES);
     if (acc)
-        hipLaunchKernelGGL((gemv_fast_q4k<true, D, WAVES, KS>), grid, block, lds, ctx->stream, w->planes(), x, c, N, row0, w->K);
+        hipLaunchKernelGGL((gemv_fast_q4k<true, D, WAVES, KS, R>), grid, block, lds, ctx->stream, w->planes(), x, c, N, row0, w->K);
     else
-        hipLaunchKernelGGL((gemv_fast_q4k<false, D, WAVES, KS>), grid, block, lds, ctx->stream, w->planes(), x, c, N, row0, w->K);
+        hipLaunchKernelGGL((gemv_fast_q4k<false, D, WAVES, KS, R>), grid, block, lds, ctx->stream, w->planes(), x, c, N, row0, w->K);
     return launch_check(ctx, "gemv_fast_q4k");
 }
 
@@ -171,32 +200,25 @@ int launch_gemv(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, 
 int launch_gemv_fast(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                      bool acc) {
     if (w->dtype == kQ4K) {
-        // launch shape "D,WAVES,KS": blocks in flight per lane, waves per workgroup, K parts per row group.
-        // Measured on cold 1.1 GiB rings at K = 4096: splitting K in two wins while the grid is small (1024 and
-        // 4096 rows: 5.5 / 5.9 us vs 7.9 / 8.2), whole rows per wave win from ~8192 rows up (14336 rows:
-        // 10.65 us vs 11.7). TRHIP_FAST_CFG overrides.
+        // launch shape "D,WAVES,KS,R": blocks in flight per lane, waves per workgroup, K parts per row group,
+        // rows per lane. Measured on cold 1.1 GiB rings at K = 4096: splitting K in two wins while the grid is
+        // small (1024 / 4096 rows: 5.5 / 5.9 us vs 7.9 / 8.2), whole rows per wave win from ~8192 rows
+        // (14336 rows: 10.7-11.5 us vs 11.6-11.7). More blocks in flight, more rows per lane or more waves per
+        // workgroup were all slower. TRHIP_FAST_CFG overrides.
         static const int forced = [] {
             const char *e = getenv("TRHIP_FAST_CFG");
-            int d = 0, wv = 0, ks = 0;
-            if (e && sscanf(e, "%d,%d,%d", &d, &wv, &ks) == 3) return 100 * d + 10 * wv + ks;
+            int d = 0, wv = 0, ks = 0, rr = 0;
+            if (e && sscanf(e, "%d,%d,%d,%d", &d, &wv, &ks, &rr) == 4) return 1000 * d + 100 * wv + 10 * ks + rr;
             return 0;
         }();
-        const int cfg = forced ? forced : (N >= 8192 ? 241 : 242);
+        const int cfg = forced ? forced : (N >= 8192 ? 2411 : 2421);
         switch (cfg) {
-        case 242: return run_q4k<2, 4, 2>(ctx, w, row0, N, x, c, acc);
-        case 442: return run_q4k<4, 4, 2>(ctx, w, row0, N, x, c, acc);
-        case 241: return run_q4k<2, 4, 1>(ctx, w, row0, N, x, c, acc);
-        case 441: return run_q4k<4, 4, 1>(ctx, w, row0, N, x, c, acc);
-        case 841: return run_q4k<8, 4, 1>(ctx, w, row0, N, x, c, acc);
-        case 421: return run_q4k<4, 2, 1>(ctx, w, row0, N, x, c, acc);
-        case 221: return run_q4k<2, 2, 1>(ctx, w, row0, N, x, c, acc);
-        case 282: return run_q4k<2, 8, 2>(ctx, w, row0, N, x, c, acc);
-        case 482: return run_q4k<4, 8, 2>(ctx, w, row0, N, x, c, acc);
-        case 481: return run_q4k<4, 8, 1>(ctx, w, row0, N, x, c, acc);
-        case 411: return run_q4k<4, 1, 1>(ctx, w, row0, N, x, c, acc);
-        case 811: return run_q4k<8, 1, 1>(ctx, w, row0, N, x, c, acc);
+        case 2421: return run_q4k<2, 4, 2, 1>(ctx, w, row0, N, x, c, acc);
+        case 2411: return run_q4k<2, 4, 1, 1>(ctx, w, row0, N, x, c, acc);
+        case 2422: return run_q4k<2, 4, 2, 2>(ctx, w, row0, N, x, c, acc);
+        case 8421: return run_q4k<8, 4, 2, 1>(ctx, w, row0, N, x, c, acc);
         }
-        return run_q4k<2, 4, 2>(ctx, w, row0, N, x, c, acc);
+        return run_q4k<2, 4, 2, 1>(ctx, w, row0, N, x, c, acc);
     }
     return launch_gemv(ctx, w, row0, N, x, c, acc, TRHIP_MODE_EXACT);
 }
