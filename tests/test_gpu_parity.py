@@ -118,8 +118,11 @@ def test_gemv_set_slice_unaligned(backend, dt):
     same_bits(got, want)
 
 
-@pytest.mark.parametrize("dt,N,K", [(Q4K, 14336, 4096), (Q4K, 4096, 14336), (Q6K, 1024, 4096), (Q8, 4096, 4096),
-                                    (Q4, 14336, 4096)])
+LLAMA_LINEARS = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]  # q/o, k/v, gate/up, down
+
+
+@pytest.mark.parametrize("dt,N,K", [(Q4K, n, k) for n, k in LLAMA_LINEARS] + [(Q6K, n, k) for n, k in LLAMA_LINEARS] +
+                         [(Q8, 4096, 4096), (Q4, 14336, 4096), (Q4, 4096, 14336)])
 def test_gemv_llama_shapes_bits(backend, dt, N, K):
     """Llama-3-8B shapes with encoded N(0, 0.02) weights (1% outliers for K-quants): bit-identical."""
     raw = synth.quant_weights(dt, N, K, seed=11, outliers=0.01 if dt in (Q4K, Q6K) else 0.0)
@@ -277,6 +280,40 @@ def test_actq_tiles_bits(backend, M, N, K, row0, acc):
     w.release()
 
 
+@pytest.mark.parametrize("dt,N,K,M", [(Q4, 14336, 4096, 8), (Q4, 4096, 14336, 8), (Q4K, 4096, 4096, 16),
+                                      (Q6K, 1024, 4096, 16)])
+def test_gemm_rows_llama_shapes_bits(backend, dt, N, K, M):
+    """Decode batches on Llama shapes through the fp32 M>1 path: q4_0 FFN at batch 8, q4_k / q6_k at batch 16."""
+    raw = synth.quant_weights(dt, N, K, seed=31, outliers=0.01 if dt in (Q4K, Q6K) else 0.0)
+    X = synth.activations(M, K, seed=32)
+    w = backend.FromQuantized(dt, raw, N, K)
+    xb, cb = backend.ctx.to_device(X), backend.ctx.alloc(M * N * 4)
+    backend.GemmSet(M, N, K, xb, w, cb)
+    same_bits(cb.download(np.float32, M * N), O.quant_gemm(dt, M, N, K, X, raw))
+    for b in (xb, cb):
+        b.free()
+    w.release()
+
+
+@pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336)])
+@pytest.mark.parametrize("M", [128, 512, 2048])
+def test_actq_prefill_sizes_bits(backend, N, K, M):
+    """The prefill configurations (q4_k, M in {128, 512, 2048}). Every output row is one single-row kernel result
+    (cpu_quant_q8.go:183-185), so at M = 128 all rows are compared and above that a fixed sample of rows."""
+    raw = synth.quant_weights(Q4K, N, K, seed=41, outliers=0.01)
+    X = synth.activations(M, K, seed=42 + M)
+    w = backend.FromQuantized(Q4K, raw, N, K)
+    xb, cb = backend.ctx.to_device(X), backend.ctx.alloc(M * N * 4)
+    backend.GemmActQuant(M, N, K, xb, w, cb, accumulate=False)
+    got = cb.download(np.float32, M * N).reshape(M, N)
+    rows = list(range(M)) if M <= 128 else sorted({0, 1, 63, 64, 127, M // 2 + 3, M - 65, M - 2, M - 1})
+    want = O.quant_gemm_act(Q4K, len(rows), N, K, np.ascontiguousarray(X[rows]), raw)
+    same_bits(got[rows], want)
+    for b in (xb, cb):
+        b.free()
+    w.release()
+
+
 @pytest.mark.parametrize("dt,N,K,M", [(Q4K, 14336, 4096, 16), (Q4K, 4096, 14336, 8), (Q6K, 1024, 4096, 32),
                                       (Q4, 4096, 4096, 16)])
 def test_actq_llama_shapes_bits(backend, dt, N, K, M):
@@ -348,6 +385,21 @@ def test_gemv_fast_tolerance(backend, dt, N, K):
         assert err <= FAST_TOL[dt], (dt, N, K, scale, err)
         for b in (xb, cb):
             b.free()
+    w.release()
+
+
+@pytest.mark.parametrize("N,K", LLAMA_LINEARS)
+def test_gemv_fast_llama_shapes(backend, N, K):
+    """The fast q4_k GEMV on every Llama-3-8B linear shape (encoded weights with 1% outliers) within 1e-4."""
+    raw = synth.quant_weights(Q4K, N, K, seed=51, outliers=0.01)
+    x = synth.activations(1, K, seed=52)
+    w = backend.FromQuantized(Q4K, raw, N, K)
+    xb, cb = backend.ctx.to_device(x), backend.ctx.alloc(N * 4)
+    backend.GemmSet(1, N, K, xb, w, cb, mode=MODE_FAST)
+    err = rel_err(cb.download(np.float32, N), O.quant_gemm(Q4K, 1, N, K, x, raw).reshape(-1))
+    assert err <= FAST_TOL[Q4K], err
+    for b in (xb, cb):
+        b.free()
     w.release()
 
 
