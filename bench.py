@@ -40,9 +40,9 @@ COPY_BYTES = 256 << 20
 # HBM bytes per launch of the headline kernel from rocprofv3 FETCH_SIZE + WRITE_SIZE over --profile-kernel gemv,
 # each divided by the same counter's reading per byte of the calibration copy (profiles/gemv_q4_k_14336x4096_*.txt).
 # Keyed by mode.
-TRAFFIC = {"fast": 33278109, "exact": 33434768}
+TRAFFIC = {"fast": 33274014, "exact": 33372309}
 # Same counters over --profile-kernel prefill (profiles/prefill_q4_k_14336x4096_M512.txt): quantizer + MFMA kernel.
-PREFILL_TRAFFIC = {"quantize_q8": 11181340, "actq_mfma_q4k": 100162620}
+PREFILL_TRAFFIC = {"quantize_q8": 11181340, "actq_mfma_q4k": 100187322}
 
 
 def algorithmic_bytes(n, k):
@@ -60,6 +60,8 @@ def parse():
     ap.add_argument("--prefill-m", type=int, default=512)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample (0 = skip)")
     ap.add_argument("--sweep", type=int, default=1, help="also time the 32-layer decode sweep (0 = skip)")
+    ap.add_argument("--shapes", type=int, default=1,
+                    help="also time every Llama-3-8B GEMV shape per dtype and the prefill grid (0 = skip)")
     ap.add_argument("--profile-kernel", choices=["gemv", "prefill", "copy"], default=None,
                     help="run only this kernel --steps times, eagerly (counter runs)")
     return ap.parse_args()
@@ -114,6 +116,56 @@ def decode_sweep(tb, batches, mode, replays=5):
                             "per token step, weights %d B" % (7 * N_LAYERS + 1, wbytes),
                 "mode": "fast" if mode else "exact", "weight_bytes": wbytes})
     return res
+
+
+def shape_table(tb):
+    """Cold-ring GEMV time for every Llama-3-8B linear shape and dtype (exact, plus fast for q4_k), and the prefill
+    grid M in {128, 512, 2048} x both FFN shapes. Random-code blocks (synth.random_blocks): timing only."""
+    from tcb_amd import MODE_EXACT, MODE_FAST, Q4, Q4K, Q6K, Q8, _lib, synth
+    L = _lib.lib()
+    ctx = tb.ctx
+    gemv = {}
+    cases = [(Q8, 4096, 4096), (Q4, 14336, 4096), (Q4, 4096, 14336)] + \
+            [(dt, n, k) for dt in (Q4K, Q6K) for n, k in ((4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336))]
+    names = {Q8: "q8_0", Q4: "q4_0", Q4K: "q4_k", Q6K: "q6_k"}
+    for dt, n, k in cases:
+        raw = synth.random_blocks(dt, n, k, seed=5)
+        ring = [tb.FromQuantized(dt, raw, n, k) for _ in range(max(2, -(-RING_BYTES // raw.nbytes)))]
+        xb = ctx.to_device(synth.activations(1, k, seed=6))
+        cb = ctx.alloc(n * 4)
+        res = {}
+        for md in ((MODE_EXACT, MODE_FAST) if dt == Q4K else (MODE_EXACT,)):
+            tb.GemmSet(1, n, k, xb, ring[0], cb, mode=md)
+            ctx.sync()
+            g = capture(tb, lambda: [tb.GemmSet(1, n, k, xb, w, cb, mode=md) for w in ring])
+            time_graph(tb, g, 1)
+            us = time_graph(tb, g, 3) * 1e3 / (3 * len(ring))
+            L.trhip_graph_destroy(g)
+            res["fast" if md else "exact"] = {"us": round(us, 2), "GB/s": round(raw.nbytes / us / 1e3, 1)}
+        gemv["%s %dx%d" % (names[dt], n, k)] = res
+        for w in ring:
+            w.release()
+        xb.free()
+        cb.free()
+    prefill = {}
+    for n, k in ((14336, 4096), (4096, 14336)):
+        w = tb.FromQuantized(Q4K, synth.random_blocks(Q4K, n, k, seed=7), n, k)
+        for M in (128, 512, 2048):
+            Xb = ctx.to_device(synth.activations(M, k, seed=8))
+            Cb = ctx.alloc(M * n * 4)
+            tb.GemmActQuant(M, n, k, Xb, w, Cb, accumulate=False)
+            ctx.sync()
+            g = capture(tb, lambda: tb.GemmActQuant(M, n, k, Xb, w, Cb, accumulate=False))
+            time_graph(tb, g, 2)
+            ms = time_graph(tb, g, 5) / 5
+            L.trhip_graph_destroy(g)
+            tops = 2.0 * M * n * k / (ms * 1e-3) / 1e12
+            prefill["q4_k %dx%d M=%d" % (n, k, M)] = {"us": round(ms * 1e3, 1), "int8_tops": round(tops, 1),
+                                                     "frac_of_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+            Xb.free()
+            Cb.free()
+        w.release()
+    return {"gemv_cold_ring": gemv, "prefill": prefill}
 
 
 def profile_kernel(a):
@@ -261,6 +313,7 @@ def main():
         Cb.free()
 
     sweep = decode_sweep(tb, (1, 16), mode) if a.sweep else None
+    shapes = shape_table(tb) if a.shapes else None
 
     # CPU baseline: AVX2 restatement of the reference's sdotq4k GEMV, all host cores, same bytes
     cpu = None
@@ -315,6 +368,7 @@ def main():
                      "kernel": "gemv_q4_k_%s" % a.mode, "algorithmic_bytes_per_launch": abytes},
         "prefill": prefill,
         "decode_sweep": sweep,
+        "shapes": shapes,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
