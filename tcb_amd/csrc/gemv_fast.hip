@@ -33,9 +33,9 @@ __device__ __forceinline__ void fma_nib4(float &p, uint32_t nib4, float4 xv) {
 // Eight lanes per row; lane (g, h) = (lane8 >> 1, lane8 & 1) owns the 16 qs bytes 32g + 16h .. +16 of
 // every block: low nibbles are elements 16h..16h+15 of sub-block 2g, high nibbles the same elements of
 // sub-block 2g+1. Each lane serves R rows (8 apart) with the same x, so a wave covers 8R rows and every x
-// slice read from LDS feeds R rows (LDS read bandwidth, not HBM, bounds this kernel at R = 1). A workgroup is
-// WAVES waves; with KS = 2 the waves pair up on the same rows and take one half of K each (the halves meet in
-// LDS, half 0 + half 1), with KS = 1 each wave owns its rows' whole K. The 8 lanes of a row then add with a
+// slice read from LDS feeds R rows. A workgroup is WAVES waves; with KS > 1 the waves form groups of KS on the
+// same rows, each taking one KS-th of K (the parts meet in LDS and are added in part order), with KS = 1 each
+// wave owns its rows' whole K. The 8 lanes of a row then add with a
 // fixed xor-butterfly. x lives in LDS with a 16-byte pad per 256 bytes (the 8 slices a wave reads per step
 // fall in distinct banks), its 16-element sums next to it. Weights are requested D blocks ahead, x one block
 // ahead.
@@ -44,7 +44,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_fast_q4k(const Planes p, cons
                                                             float *__restrict__ c, int64_t N, int64_t row0, int64_t K) {
     constexpr int THREADS = 64 * WAVES, ROWS = 8 * R * WAVES / KS;
     extern __shared__ float4 lds4[];
-    __shared__ float half_part[KS == 2 ? 64 * R * WAVES / 2 : 1];
+    __shared__ float part_lds[KS > 1 ? 64 * R * (WAVES / KS) * (KS - 1) : 1];
     const int nx4 = (int)(K / 4);
     float4 *xs = lds4;                                             // padded: nx4 + nx4/16 float4
     float *sx = reinterpret_cast<float *>(lds4 + nx4 + nx4 / 16);  // K/16 floats
@@ -53,8 +53,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_fast_q4k(const Planes p, cons
     const int lane8 = lane & 7, g = lane8 >> 1, hsel = lane8 & 1;
     const int rg = w / KS, part = w % KS;
     const int nb = (int)p.nb;
-    const int nh = (nb + 1) / 2;
-    const int b0 = KS == 1 ? 0 : (part ? nh : 0), b1 = KS == 1 ? nb : (part ? nb : nh);
+    const int nh = (nb + KS - 1) / KS;  // blocks per K part
+    const int b0 = part * nh < nb ? part * nh : nb, b1 = b0 + nh < nb ? b0 + nh : nb;
     int64_t r[R];
     const uint4 *hp[R], *qp[R];
 #pragma unroll
@@ -158,15 +158,18 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_fast_q4k(const Planes p, cons
             }
         }
     }
-    if (KS == 2) {
+    if (KS > 1) {  // parts 1..KS-1 hand their sums to part 0, which adds them in part order
+        constexpr int RG = WAVES / KS;
         if (part) {
 #pragma unroll
-            for (int i = 0; i < R; i++) half_part[64 * (R * rg + i) + lane] = acc[i];
+            for (int i = 0; i < R; i++) part_lds[64 * (((part - 1) * RG + rg) * R + i) + lane] = acc[i];
         }
         __syncthreads();
         if (part) return;
 #pragma unroll
-        for (int i = 0; i < R; i++) acc[i] = acc[i] + half_part[64 * (R * rg + i) + lane];
+        for (int q = 1; q < KS; q++)
+#pragma unroll
+            for (int i = 0; i < R; i++) acc[i] = acc[i] + part_lds[64 * (((q - 1) * RG + rg) * R + i) + lane];
     }
 #pragma unroll
     for (int i = 0; i < R; i++) {
@@ -201,18 +204,22 @@ int launch_gemv_fast(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_
                      bool acc) {
     if (w->dtype == kQ4K) {
         // launch shape "D,WAVES,KS,R": blocks in flight per lane, waves per workgroup, K parts per row group,
-        // rows per lane. Measured on cold 1.1 GiB rings at K = 4096: splitting K in two wins while the grid is
-        // small (1024 / 4096 rows: 5.5 / 5.9 us vs 7.9 / 8.2), whole rows per wave win from ~8192 rows
-        // (14336 rows: 10.7-11.5 us vs 11.6-11.7). More blocks in flight, more rows per lane or more waves per
-        // workgroup were all slower. TRHIP_FAST_CFG overrides.
+        // rows per lane. Measured on cold 1.1 GiB rings: splitting K wins while the grid is small (1024 / 4096 rows
+        // at K = 4096: 5.5 / 5.9 us with 2 parts vs 7.9 / 8.2 whole), whole rows per wave win from ~8192 rows
+        // (14336 rows: 10.7-11.5 us vs 11.6-11.7). More blocks in flight or more rows per lane were slower.
+        // TRHIP_FAST_CFG overrides.
         static const int forced = [] {
             const char *e = getenv("TRHIP_FAST_CFG");
             int d = 0, wv = 0, ks = 0, rr = 0;
             if (e && sscanf(e, "%d,%d,%d,%d", &d, &wv, &ks, &rr) == 4) return 1000 * d + 100 * wv + 10 * ks + rr;
             return 0;
         }();
-        const int cfg = forced ? forced : (N >= 8192 ? 2411 : 2421);
+        // K split in 4 for fewer rows (cold, us): 4096x14336 10.9 vs 14.5 (2 parts), 4096x4096 5.1 vs 6.0,
+        // 1024x14336 8.3 vs 12.8
+        const int cfg = forced ? forced : (N >= 8192 ? 2411 : (N >= 2048 ? 2841 : 2441));
         switch (cfg) {
+        case 2441: return run_q4k<2, 4, 4, 1>(ctx, w, row0, N, x, c, acc);
+        case 2841: return run_q4k<2, 8, 4, 1>(ctx, w, row0, N, x, c, acc);
         case 2421: return run_q4k<2, 4, 2, 1>(ctx, w, row0, N, x, c, acc);
         case 2411: return run_q4k<2, 4, 1, 1>(ctx, w, row0, N, x, c, acc);
         case 2422: return run_q4k<2, 4, 2, 2>(ctx, w, row0, N, x, c, acc);
