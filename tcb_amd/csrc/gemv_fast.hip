@@ -181,6 +181,251 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_fast_q4k(const Planes p, cons
     }
 }
 
+// Fixed-order sum over the 64 lanes of eight values per lane (one per row), all in VALU lane permutes: two
+// transpose levels with v_permlane32_swap / v_permlane16_swap (each swap leaves, in the two registers, the
+// halves a lane must add), a third through DPP row_ror:8, then three DPP levels inside each group of 8 lanes
+// (row_half_mirror, quad_perm [2,3,0,1], quad_perm [1,0,3,2]). Lane l ends with the full sum of row l >> 3.
+// The swap results pass through opaque(): read as floats straight from the builtin's pair, this compiler
+// folds the two halves into one register (v_add_f32 vN, vN, vN).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_sum8(float v[8], int lane) {
+    float u[4], t[2];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {  // lanes 0-31 keep row i, lanes 32-63 row i + 4
+        const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v[i]),
+                                                        __builtin_bit_cast(unsigned, v[i + 4]), false, false);
+        u[i] = __builtin_bit_cast(float, opaque(r[0])) + __builtin_bit_cast(float, opaque(r[1]));
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {  // lane bit 4 selects row +2
+        const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, u[i]),
+                                                        __builtin_bit_cast(unsigned, u[i + 2]), false, false);
+        t[i] = __builtin_bit_cast(float, opaque(r[0])) + __builtin_bit_cast(float, opaque(r[1]));
+    }
+    const bool b3 = lane & 8;  // lane bit 3 selects row +1
+    const float keep = b3 ? t[1] : t[0], send = b3 ? t[0] : t[1];
+    float a = keep + dpp_f<0x128>(send);  // row_ror:8 is lane ^ 8 inside 16 lanes
+    a = a + dpp_f<0x141>(a);              // row_half_mirror: lane ^ 7 inside 8 lanes
+    a = a + dpp_f<0x4E>(a);               // quad_perm [2,3,0,1]
+    a = a + dpp_f<0xB1>(a);               // quad_perm [1,0,3,2]
+    return a;
+}
+
+// Fixed-point x for v_dot4_i32_i8: within a 32-element half with 2^e > max|x|, X = rint(x * 2^(22-e)), so
+// |X| <= 2^22, split into signed bytes X = d2*2^16 + d1*2^8 + d0 (d0, d1 in [-128, 127], |d2| <= 65). x4_digits
+// packs the digits of four consecutive elements into three dwords (digit t of element k in byte k of
+// dword t); one unit of X weighs 2^(e-22).
+__device__ __forceinline__ void x4_digits(const float *xv, int e, uint32_t out[3]) {
+    uint32_t p0 = 0, p1 = 0, p2 = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int X = (int)rintf(ldexpf(xv[k], 22 - e));
+        const int d0 = (int)(int8_t)(X & 0xFF), x1 = (X - d0) >> 8;
+        const int d1 = (int)(int8_t)(x1 & 0xFF), d2 = (x1 - d1) >> 8;
+        p0 |= (uint32_t)(d0 & 0xFF) << (8 * k);
+        p1 |= (uint32_t)(d1 & 0xFF) << (8 * k);
+        p2 |= (uint32_t)(d2 & 0xFF) << (8 * k);
+    }
+    out[0] = p0;
+    out[1] = p1;
+    out[2] = p2;
+}
+
+// q4_k, K across lanes. A K part is up to 16 blocks; lane l of a wave owns quarter g = l & 3 of block l >> 2 of
+// its part: qs bytes 32g .. 32g+31 (the low nibbles are sub-block 2g, the high nibbles sub-block 2g+1), i.e. the
+// 64 contiguous elements 256b + 64g .. +63. Their x stays in registers for the whole kernel as fixed-point digits
+// (x4_digits), so the products with the 4-bit codes are exact integer dot products (v_dot4_i32_i8, one per digit
+// and four codes) and only the per-sub-block sums are rounded:
+//   sum_e y_e x_e = s_j * 2^(e-22) * (sum_e q_e X_e) - m_j * (sum_e x_e).
+// The fixed-point x is exact to 2^-23 of the largest |x| of its 32-element half; a lane whose x holds Inf or NaN
+// (or whose x sums overflow) takes float products of the dequantized values instead (IEEE propagation).
+//
+// A wave streams whole rows: per row, 64 lanes read 2 KB of qs (32 contiguous bytes each) and the block headers,
+// and each lane leaves one partial; eight rows' partials meet in lane_sum8. A row group (the KS waves that
+// share rows) takes rows gw, gw + G, gw + 2G, ... (G row groups in the grid, at most RPW rows each, all in
+// straight-line code so the loads' wait counts stay exact); slots past a group's last row re-read that row
+// (its own, cached) and are not stored. With KS > 1 the parts 1..KS-1 hand their row sums through LDS to
+// part 0, which adds them in part order. The RG row groups of a part share x: each loads and digitizes 16 / RG
+// of the 16 four-element columns, through LDS. Weights are requested PD rows ahead, after x.
+template <bool ACC, int WAVES, int KS, int PD, int RPW>
+__global__ __launch_bounds__(64 * WAVES) void gemv_kl_q4k(const Planes p, const float *__restrict__ x,
+                                                          float *__restrict__ c, int64_t N, int64_t row0) {
+    constexpr int RG = WAVES / KS;
+    static_assert(16 % RG == 0, "the row groups of a part split the 16 columns of x evenly");
+    constexpr int CPW = 16 / RG;
+    __shared__ float part_lds[2][KS > 1 ? (KS - 1) * RG * 8 : 1];
+    __shared__ uint32_t xd_lds[KS][16][3][64];
+    __shared__ float4 xp_lds[KS][RG][64];
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int rg = w / KS, part = w % KS;
+    const int nb = (int)p.nb;
+    const int bpp = (nb + KS - 1) / KS;
+    const int pb0 = part * bpp, pb1 = pb0 + bpp < nb ? pb0 + bpp : nb;
+    const int g = lane & 3, b = pb0 + (lane >> 2);
+    const bool active = b < pb1;
+    const int bc = active ? b : (pb0 < nb ? pb0 : nb - 1);  // inactive lanes read a valid block, add nothing
+    const float4 *x4 = reinterpret_cast<const float4 *>(x + 256 * (int64_t)bc + 64 * g);
+    // issue order: this wave's columns of x (cache-resident), then the first PD rows, so that waiting for x
+    // leaves the rows in flight
+    float4 xraw[CPW];
+#pragma unroll
+    for (int i = 0; i < CPW; i++) xraw[i] = x4[rg * CPW + i];
+    const int k0 = (2 * g) & 3, k1 = k0 + 1;
+    const uint4 *hb = reinterpret_cast<const uint4 *>(p.aux) + bc;
+    const uint4 *qb = reinterpret_cast<const uint4 *>(p.qs) + 8 * (int64_t)bc + g;  // + 4: bytes 16 .. 31
+    // row counts fit 32 bits (the launcher checks), so the uniform row arithmetic stays 32-bit
+    const uint32_t G = gridDim.x * RG, gw = blockIdx.x * RG + rg, n32 = (uint32_t)N;
+    const uint32_t nv = gw < n32 ? (n32 - 1 - gw) / G + 1 : 0;                 // rows of this row group
+    const uint32_t last = nv > 0 ? gw + (nv - 1) * G : gw - (gw / n32) * n32;  // what slots past them re-read
+    auto row_of = [&](int i) { return row0 + (int64_t)((uint32_t)i < nv ? gw + (uint32_t)i * G : last); };
+    uint4 H[PD], Q0[PD], Q1[PD];
+#pragma unroll
+    for (int s = 0; s < PD; s++) {
+        const int64_t row = row_of(s);
+        H[s] = hb[row * nb];
+        Q0[s] = qb[row * nb * 8];
+        Q1[s] = qb[row * nb * 8 + 4];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // per-wave partial sums and maxima of its columns' halves meet in LDS (added in wave order); then each wave
+    // turns its columns into digits for all 64 lanes, which every wave of the part reads back
+    int xd[2][8][3];
+    int ex[2];  // one unit of X weighs 2^ex (applied last, so subnormal x keeps its value)
+    float sxl = 0.0f, sxh = 0.0f;
+    {
+        float ps[2] = {0.0f, 0.0f}, pm[2] = {0.0f, 0.0f}, xc[CPW * 4];
+#pragma unroll
+        for (int i = 0; i < CPW; i++) {
+            const float4 t = xraw[i];
+            const float e4[4] = {active ? t.x : 0.0f, active ? t.y : 0.0f, active ? t.z : 0.0f, active ? t.w : 0.0f};
+            const int hf = (rg * CPW + i) >> 3;  // wave-uniform
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                xc[4 * i + k] = e4[k];
+                ps[hf] += e4[k];
+                pm[hf] = fmaxf(pm[hf], fabsf(e4[k]));
+            }
+        }
+        xp_lds[part][rg][lane] = make_float4(ps[0], ps[1], pm[0], pm[1]);
+        __syncthreads();
+        float m0 = 0.0f, m1 = 0.0f;
+#pragma unroll
+        for (int q = 0; q < RG; q++) {
+            const float4 t = xp_lds[part][q][lane];
+            sxl += t.x;
+            sxh += t.y;
+            m0 = fmaxf(m0, t.z);
+            m1 = fmaxf(m1, t.w);
+        }
+        int e0 = 0, e1 = 0;
+        (void)frexpf(m0, &e0);  // m = f * 2^e, f in [0.5, 1); 0 gives e = 0
+        (void)frexpf(m1, &e1);
+        ex[0] = e0 - 22;
+        ex[1] = e1 - 22;
+#pragma unroll
+        for (int i = 0; i < CPW; i++) {
+            const int col = rg * CPW + i;
+            uint32_t dg[3];
+            x4_digits(xc + 4 * i, col < 8 ? e0 : e1, dg);
+#pragma unroll
+            for (int t = 0; t < 3; t++) xd_lds[part][col][t][lane] = dg[t];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int col = 0; col < 16; col++)
+#pragma unroll
+            for (int t = 0; t < 3; t++) xd[col >> 3][col & 7][t] = (int)xd_lds[part][col][t][lane];
+    }
+    const bool fin = __builtin_isfinite(sxl) && __builtin_isfinite(sxh);  // false also when a finite sum overflows
+#pragma unroll
+    for (int i0 = 0; i0 < RPW; i0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            const int slot = s % PD;
+            const uint4 h = H[slot], q0 = Q0[slot], q1 = Q1[slot];
+            const float d = f16_to_f32((uint16_t)(h.x & 0xFFFF)), dmin = f16_to_f32((uint16_t)(h.x >> 16));
+            uint32_t sc_lo, sc_hi, m_lo, m_hi;
+            q4k_scales(h.y, h.z, h.w, sc_lo, sc_hi, m_lo, m_hi);
+            const uint32_t scw = g < 2 ? sc_lo : sc_hi, mw = g < 2 ? m_lo : m_hi;
+            const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+            const float s0 = d * ubyte_f(scw, k0), n0 = -(dmin * ubyte_f(mw, k0));
+            const float s1 = d * ubyte_f(scw, k1), n1 = -(dmin * ubyte_f(mw, k1));
+            int l0 = 0, l1 = 0, l2 = 0, h0 = 0, h1 = 0, h2 = 0;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int lo = (int)(qw[k] & 0x0F0F0F0Fu), hi = (int)((qw[k] >> 4) & 0x0F0F0F0Fu);
+                l0 = __builtin_amdgcn_sdot4(lo, xd[0][k][0], l0, false);
+                l1 = __builtin_amdgcn_sdot4(lo, xd[0][k][1], l1, false);
+                l2 = __builtin_amdgcn_sdot4(lo, xd[0][k][2], l2, false);
+                h0 = __builtin_amdgcn_sdot4(hi, xd[1][k][0], h0, false);
+                h1 = __builtin_amdgcn_sdot4(hi, xd[1][k][1], h1, false);
+                h2 = __builtin_amdgcn_sdot4(hi, xd[1][k][2], h2, false);
+            }
+            // |l1| * 256 + |l0| < 2^24: the first two digits add exactly
+            const float pl = fmaf((float)l2, 65536.0f, fmaf((float)l1, 256.0f, (float)l0));
+            const float ph = fmaf((float)h2, 65536.0f, fmaf((float)h1, 256.0f, (float)h0));
+            float a = ldexpf(s0 * pl, ex[0]);
+            a = fmaf(n0, sxl, a);
+            a = a + ldexpf(s1 * ph, ex[1]);
+            a = fmaf(n1, sxh, a);
+            if (!fin) {  // Inf or NaN in this lane's x: dequantized values times x in float
+                a = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const float4 xl = x4[k], xh = x4[8 + k];
+                    const uint32_t lo = qw[k] & 0x0F0F0F0Fu, hi = (qw[k] >> 4) & 0x0F0F0F0Fu;
+                    const float xlv[4] = {xl.x, xl.y, xl.z, xl.w}, xhv[4] = {xh.x, xh.y, xh.z, xh.w};
+#pragma unroll
+                    for (int t = 0; t < 4; t++) {
+                        a = fmaf(fmaf(s0, ubyte_f(lo, t), n0), xlv[t], a);
+                        a = fmaf(fmaf(s1, ubyte_f(hi, t), n1), xhv[t], a);
+                    }
+                }
+            }
+            v[s] = active ? a : 0.0f;
+            if (i0 + s + PD < RPW) {  // refill the slot just consumed
+                const int64_t row = row_of(i0 + s + PD);
+                H[slot] = hb[row * nb];
+                Q0[slot] = qb[row * nb * 8];
+                Q1[slot] = qb[row * nb * 8 + 4];
+            }
+        }
+        float sum = lane_sum8(v, lane);
+        const int ri = lane >> 3;
+        if (KS > 1) {
+            float *pl = part_lds[(i0 >> 3) & 1];
+            if (part && (lane & 7) == 0) pl[((part - 1) * RG + rg) * 8 + ri] = sum;
+            __syncthreads();
+            if (!part) {
+#pragma unroll
+                for (int q = 1; q < KS; q++) sum = sum + pl[((q - 1) * RG + rg) * 8 + ri];
+            }
+        }
+        const int64_t r = gw + (int64_t)(i0 + ri) * G;
+        if (part == 0 && (lane & 7) == 0 && (uint32_t)(i0 + ri) < nv) c[r] = ACC ? c[r] + sum : sum;
+    }
+}
+
+template <int WAVES, int KS, int PD, int RPW>
+int run_kl(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c, bool acc) {
+    constexpr int RG = WAVES / KS;
+    if ((w->nb + KS - 1) / KS > 16) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv_kl: K parts of more than 16 blocks");
+    const int64_t wgs = (N + RG * RPW - 1) / (RG * RPW);  // every row group gets at most RPW rows
+    if (N >= (int64_t)1 << 31 || wgs * RG >= (int64_t)1 << 31)
+        return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv_kl: more than 2^31 rows");
+    dim3 grid((unsigned)wgs), block(64 * WAVES);
+    if (acc)
+        hipLaunchKernelGGL((gemv_kl_q4k<true, WAVES, KS, PD, RPW>), grid, block, 0, ctx->stream, w->planes(), x, c, N, row0);
+    else
+        hipLaunchKernelGGL((gemv_kl_q4k<false, WAVES, KS, PD, RPW>), grid, block, 0, ctx->stream, w->planes(), x, c, N, row0);
+    return launch_check(ctx, "gemv_kl_q4k");
+}
+
 template <int D, int WAVES, int KS, int R>
 int run_q4k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c, bool acc) {
     constexpr int ROWS = 8 * R * WAVES / KS;
@@ -203,6 +448,23 @@ int launch_gemv(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, 
 int launch_gemv_fast(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                      bool acc) {
     if (w->dtype == kQ4K) {
+        // K across lanes: "WAVES,KS,PD,RPW" from TRHIP_KL (read on every call, for tuning) forces that kernel
+        const char *kl = getenv("TRHIP_KL");
+        int wv = 0, ks = 0, pd = 0, rpw = 0;
+        if (kl && sscanf(kl, "%d,%d,%d,%d", &wv, &ks, &pd, &rpw) == 4) {
+            switch (10000 * wv + 1000 * ks + 10 * pd + rpw / 8) {
+            case 41041: return run_kl<4, 1, 4, 8>(ctx, w, row0, N, x, c, acc);
+            case 41042: return run_kl<4, 1, 4, 16>(ctx, w, row0, N, x, c, acc);
+            case 41022: return run_kl<4, 1, 2, 16>(ctx, w, row0, N, x, c, acc);
+            case 81041: return run_kl<8, 1, 4, 8>(ctx, w, row0, N, x, c, acc);
+            case 42042: return run_kl<4, 2, 4, 16>(ctx, w, row0, N, x, c, acc);
+            case 84041: return run_kl<8, 4, 4, 8>(ctx, w, row0, N, x, c, acc);
+            }
+            return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv_kl: no such launch shape");
+        }
+        // Measured on cold 1.1 GiB rings (us): 14336 x 4096 8.6-8.9 K across lanes vs 11.6-12.2 row-sliced;
+        // at 4096 or fewer rows, or K > 4096, the row-sliced kernel below is faster.
+        if (N >= 8192 && w->nb >= 8 && w->nb <= 16) return run_kl<4, 1, 4, 16>(ctx, w, row0, N, x, c, acc);
         // launch shape "D,WAVES,KS,R": blocks in flight per lane, waves per workgroup, K parts per row group,
         // rows per lane. Measured on cold 1.1 GiB rings: splitting K wins while the grid is small (1024 / 4096 rows
         // at K = 4096: 5.5 / 5.9 us with 2 parts vs 7.9 / 8.2 whole), whole rows per wave win from ~8192 rows

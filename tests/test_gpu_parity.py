@@ -422,3 +422,106 @@ def test_gemv_fast_deterministic_and_sliced(backend, dt):
     for b in (xb, cb):
         b.free()
     w.release()
+
+
+# q4_k fast GEMV with K across lanes (fixed-point x, int8 dot products); TRHIP_KL forces a launch shape
+KL_SHAPES = ["4,1,4,8", "4,1,4,16", "4,1,2,16", "8,1,4,8", "4,2,4,16", "8,4,4,8"]
+
+
+def _kl_parts(cfg):
+    return int(cfg.split(",")[1])
+
+
+@pytest.mark.parametrize("cfg", KL_SHAPES)
+@pytest.mark.parametrize("N,K,row0", [(1, 256, 0), (37, 1024, 0), (300, 4096, 5), (129, 3840, 0), (9000, 4096, 100),
+                                      (70, 14336, 3), (40, 8192, 0)])
+def test_gemv_kl_tolerance(backend, monkeypatch, cfg, N, K, row0):
+    """Every launch shape of the K-across-lanes kernel on ragged shapes (rows fewer than row groups, partial K
+    parts, a row slice), set and accumulate, x1 and x1000 activations: within 1e-4 of the oracle. Shapes whose
+    K needs more than 16 blocks per part are refused."""
+    monkeypatch.setenv("TRHIP_KL", cfg)
+    rows = N
+    raw = synth.quant_weights(Q4K, N + row0, K, seed=N + K, outliers=0.01)
+    w = backend.FromQuantized(Q4K, raw, N + row0, K)
+    if -(-(K // 256) // _kl_parts(cfg)) > 16:
+        xb, cb = backend.ctx.alloc(K * 4), backend.ctx.alloc(rows * 4)
+        with pytest.raises(TrhipError) as e:
+            backend.GemmSet(1, rows, K, xb, w, cb, row0=row0, mode=MODE_FAST)
+        assert e.value.code == 5
+        for b in (xb, cb):
+            b.free()
+        w.release()
+        return
+    sub = raw.reshape(N + row0, -1)[row0:].reshape(-1)
+    for scale, acc in ((1.0, False), (1000.0, True)):
+        x = synth.activations(1, K, seed=K + 1) * np.float32(scale)
+        c0 = synth.activations(1, rows, seed=rows).reshape(-1)
+        xb, cb = backend.ctx.to_device(x), backend.ctx.to_device(c0)
+        if acc:
+            backend.Gemm(1, rows, K, xb, w, cb, row0=row0, mode=MODE_FAST)
+        else:
+            backend.GemmSet(1, rows, K, xb, w, cb, row0=row0, mode=MODE_FAST)
+        want = O.quant_gemm(Q4K, 1, rows, K, x, sub, c0 if acc else None).reshape(-1)
+        err = rel_err(cb.download(np.float32, rows) / scale, want / scale)
+        assert err <= FAST_TOL[Q4K], (cfg, N, K, row0, scale, err)
+        for b in (xb, cb):
+            b.free()
+    w.release()
+
+
+@pytest.mark.parametrize("cfg", ["4,1,4,16", "8,4,4,8"])
+def test_gemv_kl_activation_range(backend, monkeypatch, cfg):
+    """Fixed-point x is scaled per 32-element half: one huge element among tiny ones, an all-zero half, and
+    subnormal activations stay within tolerance (zero x gives zero rows)."""
+    monkeypatch.setenv("TRHIP_KL", cfg)
+    N, K = 64, 4096 if _kl_parts(cfg) == 1 else 14336
+    raw = synth.quant_weights(Q4K, N, K, seed=8, outliers=0.01)
+    w = backend.FromQuantized(Q4K, raw, N, K)
+    rng = _rng(3)
+    xs = []
+    x = (rng.standard_normal(K) * 1e-3).astype(np.float32)
+    x[5], x[700] = 1e4, -3e3
+    x[64:96] = 0
+    xs.append(x)
+    xs.append((rng.standard_normal(K) * 1e-40).astype(np.float32))  # subnormal
+    xs.append(np.zeros(K, np.float32))
+    xs.append((rng.standard_normal(K) * 1e30).astype(np.float32))
+    for x in xs:
+        xb, cb = backend.ctx.to_device(x), backend.ctx.alloc(N * 4)
+        backend.GemmSet(1, N, K, xb, w, cb, mode=MODE_FAST)
+        got = cb.download(np.float32, N)
+        want = O.quant_gemm(Q4K, 1, N, K, x, raw).reshape(-1)
+        amax = float(np.max(np.abs(x))) or 1.0
+        if amax < 1e-30:
+            # subnormal products: the oracle's own K fused steps each round to the 2^-149 grid
+            assert float(np.max(np.abs(got.astype(np.float64) - want))) <= K * 2.0 ** -149
+        else:
+            assert rel_err(got / amax, want / amax) <= FAST_TOL[Q4K]
+        if not x.any():
+            assert not got.any()
+        for b in (xb, cb):
+            b.free()
+    w.release()
+
+
+@pytest.mark.parametrize("cfg", ["4,1,4,16", "8,4,4,8"])
+@pytest.mark.parametrize("bad", [np.inf, -np.inf, np.nan])
+def test_gemv_kl_non_finite(backend, monkeypatch, cfg, bad):
+    """Inf or NaN in x takes float products in the lanes that hold it: every row is NaN or +-Inf exactly where the
+    bit-exact GEMV is (a zero weight times Inf is NaN, as on the CPU)."""
+    monkeypatch.setenv("TRHIP_KL", cfg)
+    N, K = 48, 4096 if _kl_parts(cfg) == 1 else 14336
+    raw = synth.quant_weights(Q4K, N, K, seed=4, outliers=0.01)
+    w = backend.FromQuantized(Q4K, raw, N, K)
+    x = synth.activations(1, K, seed=5).reshape(-1)
+    x[1234] = bad
+    xb, cb, eb = backend.ctx.to_device(x), backend.ctx.alloc(N * 4), backend.ctx.alloc(N * 4)
+    backend.GemmSet(1, N, K, xb, w, cb, mode=MODE_FAST)
+    backend.GemmSet(1, N, K, xb, w, eb, mode=MODE_EXACT)
+    got, exact = cb.download(np.float32, N), eb.download(np.float32, N)
+    assert np.array_equal(np.isnan(got), np.isnan(exact))
+    assert np.array_equal(np.isposinf(got), np.isposinf(exact))
+    assert np.array_equal(np.isneginf(got), np.isneginf(exact))
+    for b in (xb, cb, eb):
+        b.free()
+    w.release()
