@@ -99,6 +99,10 @@ int trhip_wstore_create(trhip_ctx *ctx, int dtype, const void *raw, size_t raw_b
                         int64_t K, trhip_wstore **out);
 int trhip_wstore_destroy(trhip_wstore *w); /* Releaser.Release, tensor/device.go:520-522 */
 int trhip_wstore_info(const trhip_wstore *w, int *dtype, int64_t *N, int64_t *K, size_t *device_bytes);
+/* One store holding the rows of several (same dtype and K), in order: the merged layers of
+ * lib/layers.tr (gate_up_proj = [gate | up], layers.tr:240-262; merged q/k/v weights) as one
+ * device store, so one GEMV reads the shared activation once. The parts stay valid. */
+int trhip_wstore_concat(trhip_ctx *ctx, const trhip_wstore *const *parts, int nparts, trhip_wstore **out);
 /* RawBackend.ToRaw (tensor/typed.go:27): the original GGUF bytes of rows [row0, row0+rows). */
 int trhip_wstore_to_raw(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t rows, void *raw_out);
 
@@ -133,6 +137,17 @@ int trhip_open_q(trhip_ctx *ctx, const trhip_wstore *w, int64_t elem_off, int64_
  * a Go []int). Indices are checked on the host before upload; an out-of-range index returns
  * TRHIP_ERR_INVALID (H3043). The call waits until the indices are on the device. */
 int trhip_embedding_q(trhip_ctx *ctx, const trhip_wstore *w, const int64_t *idx, int64_t nidx, float *out);
+
+/* SwiGLU gate (lib/layers.tr:223 swiglu_gate on the [gate | up] halves of a merged gate_up output,
+ * layers.tr:240-262): out[m, i] = silu(gu[m, i]) * gu[m, I + i] for a [M, 2I] row-major gu, with silu as
+ * tensor/cpu_elementwise_wide.go:101-116 and e^x as the AVX2 expVec (tensor/cpu_vector_amd64.s:13-38):
+ * bit-identical to the CPU path. */
+int trhip_swiglu(trhip_ctx *ctx, const float *gu, int64_t M, int64_t I, float *out);
+
+/* SwiGLU.forward's first half on a merged store (lib/layers.tr:264-266): gu = x @ w^T over all 2I rows
+ * ([gate | up], trhip_gemm_q semantics and mode), then out = trhip_swiglu(gu). out is [M, I]. */
+int trhip_gemm_q_swiglu(trhip_ctx *ctx, const trhip_wstore *w, const float *x, float *out, int64_t M,
+                        int64_t K, int mode);
 
 /* Quantize fp32 rows to Q8 activation blocks on the device (tensor/cpu_quant_q8.go:39-68):
  * q [M, K] int8, d [M, K/blk] fp32, bs [M, K/16] int16; blk is 32 or 256. Exposed for

@@ -505,3 +505,45 @@ uint64_t trq_fnv1a64_f32(const float *y, size_t n) {
     }
     return h;
 }
+
+/* ------------------------------------------------------------------ SwiGLU epilogue
+ * e^x as the reference's AVX2 expVec computes it (cpu_vector_amd64.s:13-38, the UST macro, used by
+ * expVec in cpu_vector_amd64.go:31-47 for every element, tail included): clamp to [-104, 89] (a NaN
+ * input takes the lower bound and is put back at the end), n = rne(x * log2e), r = x - n*ln2 in two
+ * fused steps, a degree-6 polynomial in fused steps, and 2^n applied as two factors 2^(n>>1) and
+ * 2^(n - n>>1). The constants are the reference's (cpu_math.go:10-17, 43-50; the Cephes expf set). */
+float trq_exp_vec(float x) {
+    float x1 = x > -104.0f ? x : -104.0f;
+    x1 = x1 < 89.0f ? x1 : 89.0f;
+    const float n = rintf(x1 * 1.44269504088896341f);
+    float r = fmaf(-n, 0.693359375f, x1);
+    r = fmaf(-n, -2.12194440e-4f, r);
+    float p = 1.9875691500e-4f;
+    p = fmaf(p, r, 1.3981999507e-3f);
+    p = fmaf(p, r, 8.3334519073e-3f);
+    p = fmaf(p, r, 4.1665795894e-2f);
+    p = fmaf(p, r, 1.6666665459e-1f);
+    p = fmaf(p, r, 5.0000001201e-1f);
+    const float z = r * r;
+    p = fmaf(z, p, r);
+    float y = p + 1.0f;
+    const int ni = (int)n, h = ni >> 1, l = ni - h;
+    y = y * bits_f32((uint32_t)(h + 127) << 23);
+    y = y * bits_f32((uint32_t)(l + 127) << 23);
+    return x != x ? x : y;
+}
+
+/* x * sigma(x) as siluForward (cpu_elementwise_wide.go:101-116) with sigmoidBlock (:83-98):
+ * e = e^-|x|, sigma = 1/(1+e) for x >= 0, e/(1+e) otherwise; sigma == 0 gives +0. */
+float trq_silu(float x) {
+    const float e = trq_exp_vec(-fabsf(x));
+    const float s = x >= 0.0f ? 1.0f / (1.0f + e) : e / (1.0f + e);
+    return (s == 0.0f ? 0.0f : x) * s;
+}
+
+/* swiglu_gate (lib/layers.tr:223): silu(g) * u on a [M, 2I] row-major [G | U] buffer
+ * (the merged gate_up layout, layers.tr:240-262 and its .split(2)). */
+void trq_swiglu(const float *gu, size_t M, size_t I, float *out) {
+    for (size_t m = 0; m < M; m++)
+        for (size_t i = 0; i < I; i++) out[m * I + i] = trq_silu(gu[m * 2 * I + i]) * gu[m * 2 * I + I + i];
+}

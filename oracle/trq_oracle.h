@@ -95,6 +95,12 @@ void trq_quant_embedding(int dt, const uint8_t *raw, size_t D, const int64_t *id
 void trq_random_quant(int dt, uint32_t seed, size_t blocks, uint8_t *out);
 uint64_t trq_fnv1a64_f32(const float *y, size_t n);
 
+/* SwiGLU epilogue: e^x as the reference's AVX2 expVec (cpu_vector_amd64.s:13-38), silu as siluForward
+ * (cpu_elementwise_wide.go:101-116), and silu(g) * u over a [M, 2I] [G | U] buffer (lib/layers.tr:223). */
+float trq_exp_vec(float x);
+float trq_silu(float x);
+void trq_swiglu(const float *gu, size_t M, size_t I, float *out);
+
 /* AVX2/FMA/F16C restatements of the reference's assembly (trq_avx2.c): the CPU baseline.
  * They follow the .s instruction sequences and must agree bitwise with the scalar oracle. */
 int trq_avx2_available(void);

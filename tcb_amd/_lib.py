@@ -42,11 +42,14 @@ SIGNATURES = [
     ("trhip_wstore_destroy", INT, [P]),
     ("trhip_wstore_info", INT, [P, ctypes.POINTER(INT), ctypes.POINTER(I64), ctypes.POINTER(I64), ctypes.POINTER(SZ)]),
     ("trhip_wstore_to_raw", INT, [P, P, I64, I64, P]),
+    ("trhip_wstore_concat", INT, [P, P, INT, ctypes.POINTER(P)]),
     ("trhip_gemm_q", INT, [P, P, I64, I64, P, P, I64, I64, INT, INT]),
     ("trhip_gemm_q_actq", INT, [P, P, I64, I64, P, P, I64, I64, INT]),
     ("trhip_open_q", INT, [P, P, I64, I64, P]),
     ("trhip_embedding_q", INT, [P, P, P, I64, P]),
     ("trhip_quantize_q8", INT, [P, P, I64, I64, INT, P, P, P]),
+    ("trhip_swiglu", INT, [P, P, I64, I64, P]),
+    ("trhip_gemm_q_swiglu", INT, [P, P, P, P, I64, I64, INT]),
 ]
 
 # Status codes and enums (include/trhip.h)

@@ -139,11 +139,23 @@ class QuantWeight:
         self.ctx = ctx
         self.dt = dtype_code(dt)
         self.N, self.K = int(N), int(K)
+        if raw is None:  # filled by the caller (Concat)
+            self.h = P()
+            return
         raw = np.ascontiguousarray(raw, dtype=np.uint8)
         h = P()
         _check(_lib.lib().trhip_wstore_create(ctx.h, self.dt, raw.ctypes.data_as(P), raw.nbytes, self.N, self.K, ctypes.byref(h)), ctx.h)
         ctx.sync()  # the host bytes may be released after this returns
         self.h = h
+
+    @staticmethod
+    def Concat(parts):
+        """One store with the rows of `parts` in order (a merged layer: [gate | up], [q | k | v])."""
+        ctx = parts[0].ctx
+        w = QuantWeight(ctx, parts[0].dt, None, sum(p.N for p in parts), parts[0].K)
+        hs = (P * len(parts))(*[p.h for p in parts])
+        _check(_lib.lib().trhip_wstore_concat(ctx.h, hs, len(parts), ctypes.byref(w.h)), ctx.h)
+        return w
 
     def ToRaw(self, row0=0, rows=None):
         rows = self.N - row0 if rows is None else rows
@@ -188,6 +200,14 @@ class QuantBackend:
 
     def GemmActQuant(self, M, N, K, a, w, c, row0=0, accumulate=True):
         _check(_lib.lib().trhip_gemm_q_actq(self.ctx.h, w.h, row0, N, _ptr(a), _ptr(c), M, K, 1 if accumulate else 0), self.ctx.h)
+
+    def SwiGLU(self, gu, M, I, out):
+        """out[m, i] = silu(gu[m, i]) * gu[m, I + i] (lib/layers.tr:223 on a merged [gate | up] output)."""
+        _check(_lib.lib().trhip_swiglu(self.ctx.h, _ptr(gu), M, I, _ptr(out)), self.ctx.h)
+
+    def GemmSwiGLU(self, M, K, a, w, out, mode=MODE_EXACT):
+        """SwiGLU of x @ w^T for a merged [gate | up] store of 2I rows; out is [M, I]."""
+        _check(_lib.lib().trhip_gemm_q_swiglu(self.ctx.h, w.h, _ptr(a), _ptr(out), M, K, mode), self.ctx.h)
 
     def OpenQuant(self, out, w, offset=0, n=None):
         n = w.N * w.K - offset if n is None else n

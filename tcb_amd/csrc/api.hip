@@ -50,6 +50,26 @@ void *workspace(trhip_ctx *ctx, size_t bytes, int *status) {
     return ctx->ws;
 }
 
+void *workspace2(trhip_ctx *ctx, size_t bytes, int *status) {
+    *status = TRHIP_OK;
+    if (bytes <= ctx->ws2_bytes) return ctx->ws2;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(ctx->stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
+        *status = fail(ctx, TRHIP_ERR_INVALID, "workspace must be sized by an eager call before graph capture");
+        return nullptr;
+    }
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) { *status = hip_fail(ctx, e, "workspace sync"); return nullptr; }
+    if (ctx->ws2) (void)hipFree(ctx->ws2);
+    ctx->ws2 = nullptr;
+    ctx->ws2_bytes = 0;
+    size_t want = bytes < (size_t)(1 << 20) ? (size_t)(1 << 20) : bytes + bytes / 4;
+    e = hipMalloc(&ctx->ws2, want);
+    if (e != hipSuccess) { ctx->ws2 = nullptr; *status = hip_fail(ctx, e, "workspace alloc"); return nullptr; }
+    ctx->ws2_bytes = want;
+    return ctx->ws2;
+}
+
 __global__ void zero_f32_kernel(float *__restrict__ p, int64_t n) {
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = 0.0f;
@@ -151,6 +171,7 @@ int trhip_destroy(trhip_ctx *ctx) {
     DevGuard g(ctx);
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->ws2) (void)hipFree(ctx->ws2);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return TRHIP_OK;
@@ -345,6 +366,72 @@ int trhip_wstore_create(trhip_ctx *ctx, int dtype, const void *raw, size_t raw_b
     return TRHIP_OK;
 }
 
+int trhip_wstore_concat(trhip_ctx *ctx, const trhip_wstore *const *parts, int nparts, trhip_wstore **out) {
+    if (!ctx || !out) return TRHIP_ERR_INVALID;
+    *out = nullptr;
+    if (!parts || nparts < 1) return fail(ctx, TRHIP_ERR_INVALID, "wstore_concat: no parts");
+    const trhip_wstore *p0 = parts[0];
+    if (!p0) return fail(ctx, TRHIP_ERR_INVALID, "wstore_concat: null part");
+    int64_t N = 0;
+    for (int i = 0; i < nparts; i++) {
+        const trhip_wstore *p = parts[i];
+        if (!p || p->ctx != ctx) return fail(ctx, TRHIP_ERR_INVALID, "wstore_concat: part of another context");
+        if (p->dtype != p0->dtype || p->K != p0->K)
+            return fail(ctx, TRHIP_ERR_INVALID, "wstore_concat: parts differ in dtype or K");
+        N += p->N;
+    }
+    DevGuard g(ctx);
+    trhip_wstore *w = new (std::nothrow) trhip_wstore();
+    if (!w) return TRHIP_ERR_OOM;
+    const int dtype = p0->dtype;
+    w->ctx = ctx;
+    w->dtype = dtype;
+    w->N = N;
+    w->K = p0->K;
+    w->nb = p0->nb;
+    size_t nblk = (size_t)(N * w->nb);
+    size_t o_aux = align_up(nblk * qs_bytes(dtype), 256);
+    size_t o_sc = align_up(o_aux + nblk * aux_bytes(dtype), 256);
+    size_t o_d = align_up(o_sc + nblk * sc_bytes(dtype), 256);
+    size_t total = align_up(o_d + nblk * d_bytes(dtype), 256);
+    hipError_t e = hipMalloc(&w->base, total ? total : 256);
+    if (e != hipSuccess) {
+        delete w;
+        return hip_fail(ctx, e, "wstore_concat alloc");
+    }
+    w->bytes = total;
+    w->qs = w->base;
+    w->aux = aux_bytes(dtype) ? w->base + o_aux : nullptr;
+    w->sc = sc_bytes(dtype) ? w->base + o_sc : nullptr;
+    w->d = d_bytes(dtype) ? reinterpret_cast<uint16_t *>(w->base + o_d) : nullptr;
+    // every plane is row-major over blocks, so the rows of the parts follow each other plane by plane
+    size_t at = 0;
+    for (int i = 0; i < nparts && e == hipSuccess; i++) {
+        const trhip_wstore *p = parts[i];
+        const size_t nbk = (size_t)(p->N * p->nb);
+        if (nbk == 0) continue;
+        e = hipMemcpyAsync(w->qs + at * qs_bytes(dtype), p->qs, nbk * qs_bytes(dtype), hipMemcpyDeviceToDevice, ctx->stream);
+        if (e == hipSuccess && aux_bytes(dtype))
+            e = hipMemcpyAsync(w->aux + at * aux_bytes(dtype), p->aux, nbk * aux_bytes(dtype), hipMemcpyDeviceToDevice,
+                               ctx->stream);
+        if (e == hipSuccess && sc_bytes(dtype))
+            e = hipMemcpyAsync(w->sc + at * sc_bytes(dtype), p->sc, nbk * sc_bytes(dtype), hipMemcpyDeviceToDevice,
+                               ctx->stream);
+        if (e == hipSuccess && d_bytes(dtype))
+            e = hipMemcpyAsync(reinterpret_cast<uint8_t *>(w->d) + at * d_bytes(dtype), p->d, nbk * d_bytes(dtype),
+                               hipMemcpyDeviceToDevice, ctx->stream);
+        at += nbk;
+    }
+    if (e != hipSuccess) {
+        (void)hipStreamSynchronize(ctx->stream);
+        (void)hipFree(w->base);
+        delete w;
+        return hip_fail(ctx, e, "wstore_concat copy");
+    }
+    *out = w;
+    return TRHIP_OK;
+}
+
 int trhip_wstore_destroy(trhip_wstore *w) {
     if (!w) return TRHIP_ERR_INVALID;
     DevGuard g(w->ctx);
@@ -402,6 +489,31 @@ int trhip_gemm_q(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N,
         return launch_gemv(ctx, w, row0, N, xa, c, accumulate != 0, mode);
     }
     return launch_gemm_rows(ctx, w, row0, N, x, c, M, accumulate != 0);
+}
+
+int trhip_swiglu(trhip_ctx *ctx, const float *gu, int64_t M, int64_t I, float *out) {
+    if (!ctx) return TRHIP_ERR_INVALID;
+    if (M < 0 || I < 0) return fail(ctx, TRHIP_ERR_INVALID, "swiglu: negative size");
+    if (M == 0 || I == 0) return TRHIP_OK;
+    if (!gu || !out) return fail(ctx, TRHIP_ERR_INVALID, "swiglu: null pointer");
+    DevGuard g(ctx);
+    return launch_swiglu(ctx, gu, M, I, out);
+}
+
+int trhip_gemm_q_swiglu(trhip_ctx *ctx, const trhip_wstore *w, const float *x, float *out, int64_t M, int64_t K,
+                        int mode) {
+    if (!ctx || !w) return TRHIP_ERR_INVALID;
+    if (w->N % 2 != 0) return fail(ctx, TRHIP_ERR_INVALID, "gemm_q_swiglu: the store must hold [gate | up] rows");
+    if (M < 0 || K != w->K) return fail(ctx, TRHIP_ERR_INVALID, "gemm_q_swiglu: shape does not match the store");
+    const int64_t I = w->N / 2;
+    if (M == 0 || I == 0) return TRHIP_OK;
+    if (!x || !out) return fail(ctx, TRHIP_ERR_INVALID, "gemm_q_swiglu: null x or out");
+    DevGuard g(ctx);
+    int st = TRHIP_OK;
+    float *gu = static_cast<float *>(workspace2(ctx, (size_t)(M * w->N) * sizeof(float), &st));
+    if (!gu) return st;
+    if ((st = trhip_gemm_q(ctx, w, 0, w->N, x, gu, M, K, 0, mode)) != TRHIP_OK) return st;
+    return launch_swiglu(ctx, gu, M, I, out);
 }
 
 int trhip_quantize_q8(trhip_ctx *ctx, const float *x, int64_t M, int64_t K, int blk, int8_t *q, float *d,

@@ -146,6 +146,10 @@ struct trhip_ctx {
     // Grow-only device workspace (activation copies, quantized activations).
     void *ws = nullptr;
     size_t ws_bytes = 0;
+    // A second one for results an entry point keeps while it calls another that uses the first
+    // (the merged gate_up output of trhip_gemm_q_swiglu).
+    void *ws2 = nullptr;
+    size_t ws2_bytes = 0;
     int sm_count = 0;
 };
 
@@ -166,9 +170,11 @@ int fail(trhip_ctx *ctx, int code, const std::string &msg);
 int hip_fail(trhip_ctx *ctx, hipError_t e, const char *what);
 int launch_check(trhip_ctx *ctx, const char *what);
 void *workspace(trhip_ctx *ctx, size_t bytes, int *status);
+void *workspace2(trhip_ctx *ctx, size_t bytes, int *status);
 
 // Kernel launchers (one per source file). All return TRHIP_OK or an error code.
 int launch_repack(trhip_ctx *ctx, trhip_wstore *w, const uint8_t *raw_dev);
+int launch_swiglu(trhip_ctx *ctx, const float *gu, int64_t M, int64_t I, float *out);
 int launch_unpack(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t rows, uint8_t *raw_dev);
 int launch_dequant(trhip_ctx *ctx, const trhip_wstore *w, int64_t block0, int64_t nblocks, float *out);
 int launch_embedding(trhip_ctx *ctx, const trhip_wstore *w, const int64_t *idx, int64_t nidx, float *out,

@@ -48,6 +48,10 @@ def lib():
         L.trq_quantize_q8.argtypes = [P, SZ, ctypes.c_int, P, P, P]
         L.trq_block_isums.argtypes = [ctypes.c_int, SZ, P, P, P, P, P]
         L.trq_quant_embedding.argtypes = [ctypes.c_int, P, SZ, P, SZ, P]
+        for name in ("trq_exp_vec", "trq_silu"):
+            getattr(L, name).restype = ctypes.c_float
+            getattr(L, name).argtypes = [ctypes.c_float]
+        L.trq_swiglu.argtypes = [P, SZ, SZ, P]
         _L = L
     return _L
 
@@ -154,3 +158,23 @@ def embedding(dt, raw, D, idx):
     out = np.zeros(idx.size * D, np.float32)
     lib().trq_quant_embedding(dt, _p(raw), D, _p(idx), idx.size, _p(out))
     return out.reshape(idx.size, D)
+
+
+def exp_vec(x):
+    """e^x elementwise as the reference's AVX2 expVec (scalar loop over trq_exp_vec)."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    f = lib().trq_exp_vec
+    return np.array([f(float(v)) for v in x], np.float32)
+
+
+def silu(x):
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    f = lib().trq_silu
+    return np.array([f(float(v)) for v in x], np.float32)
+
+
+def swiglu(gu, M, I):
+    gu = np.ascontiguousarray(gu, np.float32).reshape(-1)
+    out = np.zeros(M * I, np.float32)
+    lib().trq_swiglu(_p(gu), M, I, _p(out))
+    return out.reshape(M, I)

@@ -525,3 +525,83 @@ def test_gemv_kl_non_finite(backend, monkeypatch, cfg, bad):
     for b in (xb, cb, eb):
         b.free()
     w.release()
+
+
+# ---------------------------------------------------------------- merged layers and the SwiGLU epilogue
+def test_swiglu_bits(backend):
+    """trhip_swiglu == siluForward then the product, bit for bit (layers.tr:223), on N(0, 5) values and the edge
+    values of the exp kernel's clamps, overflow, subnormals, infinities, NaN and -0."""
+    rng = _rng(21)
+    for M, I in ((3, 1000), (2, 7), (1, 1)):
+        gu = (rng.standard_normal((M, 2 * I)) * 5).astype(np.float32)
+        edge = np.array([np.inf, -np.inf, np.nan, -0.0, 0.0, -200, -103.97, -87.4, 88.5, 89, 1e-40, -1e-40, 1e30, -1e30],
+                        np.float32)
+        flat = gu.reshape(-1)
+        flat[:min(edge.size, flat.size)] = edge[:min(edge.size, flat.size)]
+        flat[-min(edge.size, flat.size):] = edge[:min(edge.size, flat.size)]
+        gb, ob = backend.ctx.to_device(gu), backend.ctx.alloc(M * I * 4)
+        backend.SwiGLU(gb, M, I, ob)
+        same_bits(ob.download(np.float32, M * I), O.swiglu(gu, M, I).reshape(-1))
+        for b in (gb, ob):
+            b.free()
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_wstore_concat(backend, dt):
+    """A merged store holds the parts' rows in order: ToRaw gives the concatenated bytes, and every GEMV / act-quant
+    GEMM on it equals the parts' results side by side (exact modes bit for bit)."""
+    K = 2 * BLOCK[dt][0] * 4
+    Ns = (37, 5, 64)
+    raws = [_weights(dt, n, K, 40 + i) for i, n in enumerate(Ns)]
+    parts = [backend.FromQuantized(dt, r, n, K) for r, n in zip(raws, Ns)]
+    w = parts[0].Concat(parts)
+    N = sum(Ns)
+    assert w.N == N
+    assert np.array_equal(w.ToRaw(), np.concatenate(raws))
+    rng = _rng(5)
+    for M in (1, 3):
+        x = _x(rng, M * K).reshape(M, K)
+        xb, cb = backend.ctx.to_device(x), backend.ctx.alloc(M * N * 4)
+        backend.GemmSet(M, N, K, xb, w, cb)
+        want = np.concatenate([O.quant_gemm(dt, M, n, K, x, r) for r, n in zip(raws, Ns)], axis=1)
+        same_bits(cb.download(np.float32, M * N), want.reshape(-1))
+        if dt != Q8:
+            backend.GemmActQuant(M, N, K, xb, w, cb, accumulate=False)
+            want = np.concatenate([O.quant_gemm_act(dt, M, n, K, x, r) for r, n in zip(raws, Ns)], axis=1)
+            same_bits(cb.download(np.float32, M * N), want.reshape(-1))
+        for b in (xb, cb):
+            b.free()
+    other = backend.FromQuantized(dt, _weights(dt, 3, 2 * K, 9), 3, 2 * K)
+    with pytest.raises(TrhipError) as e:
+        parts[0].Concat([parts[0], other])
+    assert e.value.code == 1
+    for p in parts + [w, other]:
+        p.release()
+
+
+@pytest.mark.parametrize("dt", [Q4K, Q6K, Q4])
+@pytest.mark.parametrize("M", [1, 3, 16])
+def test_gemm_q_swiglu_bits(backend, dt, M):
+    """SwiGLU.forward's gate/up half on a merged [gate | up] store: exact mode is the reference's matmul followed by
+    swiglu_gate, bit for bit; fast mode (q4_k, M = 1) within the q4_k tolerance."""
+    I, K = 300, 1024
+    graw, uraw = _weights(dt, I, K, 11), _weights(dt, I, K, 12)
+    wg, wu = backend.FromQuantized(dt, graw, I, K), backend.FromQuantized(dt, uraw, I, K)
+    w = wg.Concat([wg, wu])
+    rng = _rng(M)
+    x = _x(rng, M * K).reshape(M, K)
+    xb, ob = backend.ctx.to_device(x), backend.ctx.alloc(M * I * 4)
+    backend.GemmSwiGLU(M, K, xb, w, ob)
+    gu = np.concatenate([O.quant_gemm(dt, M, I, K, x, graw), O.quant_gemm(dt, M, I, K, x, uraw)], axis=1)
+    want = O.swiglu(gu, M, I).reshape(-1)
+    same_bits(ob.download(np.float32, M * I), want)
+    if M == 1:
+        backend.GemmSwiGLU(M, K, xb, w, ob, mode=MODE_FAST)
+        assert rel_err(ob.download(np.float32, M * I), want) <= FAST_TOL[dt]
+    odd = backend.FromQuantized(dt, _weights(dt, 3, K, 1), 3, K)
+    with pytest.raises(TrhipError):
+        backend.GemmSwiGLU(M, K, xb, odd, ob)
+    for b in (xb, ob):
+        b.free()
+    for p in (wg, wu, w, odd):
+        p.release()

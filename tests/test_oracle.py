@@ -418,3 +418,67 @@ def test_embedding_is_dequantized_rows(dt):
     assert np.array_equal(np.isnan(got), np.isnan(rows[idx]))
     fin = ~np.isnan(got)
     assert np.array_equal(got[fin].view(np.uint32), rows[idx][fin].view(np.uint32))
+
+
+# ---------------------------------------------------------------- SwiGLU epilogue (exp, silu)
+def _ulps(got, want):
+    """|got - want| in units of want's float32 spacing (cpu_math_test.go:9-23 ulpDiff)."""
+    got = np.asarray(got, np.float64)
+    want32 = np.asarray(want, np.float32)
+    sp = np.spacing(np.abs(want32)).astype(np.float64)
+    return np.abs(got - want32.astype(np.float64)) / sp
+
+
+def test_exp_vec_within_two_ulp():
+    """expVec within 2 ulp of float32(math.Exp) over the reference's own sample (cpu_math_test.go:89-120):
+    uniform [-115, 105), its edge list and small integers."""
+    rng = np.random.default_rng(43)
+    xs = (rng.random(200000) * 220 - 115).astype(np.float32)
+    edges = np.array([0, -0.0, 88.7, 88.72283, 88.7229, 89, 1000, -87.33654, -87.34, -95, -100, -103.9, -103.97,
+                      -104, -150, 1e-8, -1e-8] + [k - 4 for k in range(9)], np.float32)
+    xs = np.concatenate([xs, edges])
+    got = O.exp_vec(xs)
+    with np.errstate(over="ignore"):
+        want = np.exp(xs.astype(np.float64)).astype(np.float32)
+    fin = np.isfinite(want)
+    assert np.array_equal(got[~fin], want[~fin])
+    assert float(np.max(_ulps(got[fin], want[fin]))) <= 2
+
+
+def test_exp_vec_special_values():
+    """cpu_math_test.go:50-54: e^89 = +Inf, e^-200 = 0, e^-Inf = 0; NaN passes; e^0 = 1 exactly."""
+    got = O.exp_vec(np.array([89, -200, -np.inf, np.inf, np.nan, 0, -0.0], np.float32))
+    assert got[0] == np.inf and got[1] == 0 and got[2] == 0 and got[3] == np.inf
+    assert np.isnan(got[4]) and got[5] == 1 and got[6] == 1
+
+
+def test_silu_within_three_ulp():
+    """siluForward within 3 ulp of x / (1 + e^-x) in float64 (elementwise_wide_test.go:35-40, 69-70) on a fine
+    grid over [-20, 20] and N(0, 5) samples."""
+    rng = np.random.default_rng(7)
+    xs = np.concatenate([np.arange(-20, 20, 0.001, dtype=np.float32), (rng.standard_normal(20000) * 5).astype(np.float32)])
+    got = O.silu(xs)
+    x64 = xs.astype(np.float64)
+    want = (x64 / (1 + np.exp(-x64))).astype(np.float32)
+    assert float(np.max(_ulps(got, want))) <= 3
+
+
+def test_silu_special_values():
+    """silu(-Inf) = 0 and silu(+Inf) = +Inf (elementwise_wide_test.go:158-159); the sign of -0 stays; NaN stays;
+    large negative x gives +0 once sigma underflows (cpu_elementwise_wide.go:109-111)."""
+    got = O.silu(np.array([-np.inf, np.inf, -0.0, np.nan, -200, 0], np.float32))
+    assert got[0] == 0 and not np.signbit(got[0])
+    assert got[1] == np.inf
+    assert got[2] == 0 and np.signbit(got[2])
+    assert np.isnan(got[3])
+    assert got[4] == 0 and not np.signbit(got[4])
+    assert got[5] == 0 and not np.signbit(got[5])
+
+
+def test_swiglu_gate_is_first_half():
+    """The merged gate_up output is [G | U] per row (layers.tr:240-262 .split(2)): gate values enter silu."""
+    M, I = 3, 5
+    g = np.arange(M * I, dtype=np.float32).reshape(M, I) / 7 - 1
+    u = np.full((M, I), 2.0, np.float32)
+    out = O.swiglu(np.concatenate([g, u], axis=1), M, I)
+    assert np.array_equal(out, (O.silu(g).reshape(M, I) * np.float32(2)).astype(np.float32))
