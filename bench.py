@@ -108,8 +108,46 @@ def decode_sweep(tb, batches, mode, replays=5):
         for v in xs.values():
             v.free()
         cb.free()
+    # merged layers (the reference's merged projections, lib/layers.tr:240-262): [q | k | v] and [gate | up] as one
+    # store each, the gate/up product followed by the SwiGLU gate (trhip_gemm_q_swiglu)
+    by = {name: i for i, (name, _, _) in enumerate(LAYER)}
+    merged = []
     for layer in stores:
-        for w in layer:
+        qkv = layer[0].Concat([layer[by["q"]], layer[by["k"]], layer[by["v"]]])
+        gu = layer[0].Concat([layer[by["gate"]], layer[by["up"]]])
+        merged.append((qkv, layer[by["o"]], gu, layer[by["down"]]))
+        for name in ("q", "k", "v", "gate", "up"):
+            layer[by[name]].release()
+    ctx.sync()
+    res["merged"] = {}
+    for b in batches:
+        xs = {4096: ctx.to_device(synth.activations(b, 4096, seed=7)), 14336: ctx.to_device(synth.activations(b, 14336, seed=8))}
+        cb = ctx.alloc(b * VOCAB * 4)
+
+        def mstep():
+            for qkv, o, gu, down in merged:
+                tb.GemmSet(b, qkv.N, 4096, xs[4096], qkv, cb, mode=mode)
+                tb.GemmSet(b, 4096, 4096, xs[4096], o, cb, mode=mode)
+                tb.GemmSwiGLU(b, 4096, xs[4096], gu, cb, mode=mode)
+                tb.GemmSet(b, 4096, 14336, xs[14336], down, cb, mode=mode)
+            tb.GemmSet(b, VOCAB, HIDDEN, xs[4096], head, cb, mode=mode)
+
+        mstep()
+        ctx.sync()
+        g = capture(tb, mstep)
+        time_graph(tb, g, 1)
+        ms = time_graph(tb, g, replays) / replays
+        L.trhip_graph_destroy(g)
+        res["merged"]["batch%d" % b] = {"ms_per_token_step": round(ms, 4), "tokens_per_s": round(b / (ms * 1e-3), 1),
+                                        "weight_GB/s": round(wbytes / (ms * 1e-3) / 1e9, 1),
+                                        "hbm_frac_of_peak": round(wbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        for v in xs.values():
+            v.free()
+        cb.free()
+    res["merged"]["workload"] = ("same weights as merged layers: per layer [q | k | v] 6144x4096, o, [gate | up] 28672x4096 "
+                                 "followed by the SwiGLU gate, down; 4 weight launches + 1 SwiGLU launch per layer")
+    for m in merged:
+        for w in m:
             w.release()
     head.release()
     res.update({"workload": "32 layers x (q, k, v, o, gate, up, down) q4_k + q6_k head 128256x4096, %d GEMV launches "
