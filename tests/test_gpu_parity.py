@@ -166,6 +166,51 @@ def test_gemm_rows_bits(backend, dt, M, N, K):
     w.release()
 
 
+@pytest.mark.parametrize("dt", [Q8, Q4])
+@pytest.mark.parametrize("M,N,K", [(3, 50, 800), (16, 70, 2336), (7, 10300, 288)])
+def test_gemm_rows_short_chunk_bits(backend, dt, M, N, K):
+    """q8_0 / q4_0 rows whose last 256-wide chunk holds fewer than 8 blocks (K = 800, 2336, 288), with the chunks of
+    a row block split over workgroups (few rows) and not (10300 rows)."""
+    rng = _rng(M * 11 + K)
+    raw = _weights(dt, N, K, N + K)
+    w = backend.FromQuantized(dt, raw, N, K)
+    x = _x(rng, M * K)
+    c0 = _x(rng, M * N)
+    xb, cb = backend.ctx.to_device(x), backend.ctx.to_device(c0)
+    backend.Gemm(M, N, K, xb, w, cb)
+    same_bits(cb.download(np.float32, M * N), O.quant_gemm(dt, M, N, K, x, raw, c0))
+    for b in (xb, cb):
+        b.free()
+    w.release()
+
+
+@pytest.mark.parametrize("dt", DTS)
+@pytest.mark.parametrize("M,x_off,row0", [(33, 4, 0), (16, 8, 64), (5, 12, 3)])
+def test_gemm_rows_unaligned_slice_bits(backend, dt, M, x_off, row0):
+    """M > 1 with x at an offset that is not 16-byte aligned, a row slice of the store, and M past one pass of 16
+    activation rows; x holds infinities, a NaN, zeros and subnormals."""
+    N, K = 150, 512
+    rng = _rng(M + x_off)
+    raw = _weights(dt, N, K, M + row0)
+    w = backend.FromQuantized(dt, raw, N, K)
+    rows = N - row0 - 7
+    x = _x(rng, M * K)
+    tiny = np.array([1, 0x80000003], np.uint32).view(np.float32)
+    x[3], x[K + 1], x[2 * K + 5], x[4 * K + 9:4 * K + 11] = np.inf, -np.inf, np.nan, tiny
+    x[(M - 1) * K:(M - 1) * K + 64] = 0.0
+    c0 = _x(rng, M * rows)
+    xb = backend.ctx.alloc(M * K * 4 + 64)
+    xb.upload(x, byte_offset=x_off)
+    cb = backend.ctx.to_device(c0)
+    backend.Gemm(M, rows, K, (xb, x_off), w, cb, row0=row0)
+    rb = raw.size // N
+    want = O.quant_gemm(dt, M, rows, K, x, raw[row0 * rb:(row0 + rows) * rb], c0)
+    same_bits(cb.download(np.float32, M * rows), want)
+    for b in (xb, cb):
+        b.free()
+    w.release()
+
+
 def _edge_rows(K, blk):
     tiny = np.array([0x00400000], np.uint32).view(np.float32)[0]
     rows = []
