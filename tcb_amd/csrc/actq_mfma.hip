@@ -20,6 +20,7 @@
 // 8(v/4)+4(l/32)+v%4, column l%32) were checked on the device against host matrix products.
 #include "trhip_internal.hpp"
 
+#include <cfloat>
 #include <cstdlib>
 
 namespace trhip {
@@ -59,6 +60,31 @@ __device__ __forceinline__ uint32_t pack_h2(uint32_t a, uint32_t b) {  // two sm
            ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)b) << 16);
 }
 
+// Row states of a tile of TM activation rows from per-(row, block) NaN/Inf flags flags[row * nb + b]:
+// st[r] = 0 (finite), 1 (some block flagged) or 2 (row m0 + r is past M), *any = 1 if some row is 1. Every thread
+// takes a share of the flags, so the loads are independent rather than one chain per row. Ends with a barrier.
+template <int TM, int THREADS>
+__device__ __forceinline__ void tile_row_flags(const uint8_t *__restrict__ flags, int64_t m0, int64_t M, int nb,
+                                               int *st, int *any) {
+    const int tid = threadIdx.x;
+    if (tid < TM) st[tid] = m0 + tid < M ? 0 : 2;
+    if (tid == 0) *any = 0;
+    __syncthreads();
+    constexpr int P = THREADS / TM;  // threads per row
+    const int r = tid % TM, part = tid / TM;
+    if (m0 + r < M) {
+        const uint8_t *f = flags + (m0 + r) * nb;
+        int v = 0;
+#pragma unroll 8
+        for (int b = part; b < nb; b += P) v |= f[b];
+        if (v) {
+            atomicOr(&st[r], 1);
+            *any = 1;
+        }
+    }
+    __syncthreads();
+}
+
 // Workgroup -> tile: workgroups are dealt to the 8 XCDs round-robin, so when the tile count allows, XCD x takes a
 // contiguous run of column tiles with all their row tiles next to each other: a weight tile is fetched into that
 // XCD's L2 once and reused by every row tile.
@@ -89,19 +115,7 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(TM == 6
     int64_t tmi, tni;
     tile_of(blockIdx.x, (M + TM - 1) / TM, (N + TN - 1) / TN, tmi, tni);
     const int64_t n0 = tni * TN, m0 = tmi * TM;
-    if (tid == 0) *anybad = 0;
-    __syncthreads();
-
-    for (int i = tid; i < TM; i += THREADS) {
-        int64_t gm = m0 + i;
-        int st = 2;
-        if (gm < M) {
-            st = 0;
-            for (int b = 0; b < nb; b++) st |= bad_blk[gm * nb + b] != 0;
-            if (st) *anybad = 1;
-        }
-        rowstate[i] = st;
-    }
+    tile_row_flags<TM, THREADS>(bad_blk, m0, M, nb, rowstate, anybad);
 
     // activation staging: wave w stages chunks c = CPW w .. +CPW-1 (tile c / 8, kc c % 8), lane tid & 63 of each;
     // threads < 2 TM also stage the msum operand (tile tid >> 6), threads < TM one scale each
@@ -273,6 +287,281 @@ int run_mfma(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, con
     return launch_check(ctx, "actq_mfma_q4k");
 }
 
+// ---- Fast (tolerance) M > 1 path for q4_k: fp32 activations as three int8 digit planes ----
+//
+// The reference's GPU backend runs M > 1 as dequantized tiles through a float GEMM (gpu/backend_quant.go:43-134):
+// a tolerance path. Here each 256-wide block b of activation row m is put on a fixed-point grid,
+//   E = exponent of max|x| (max|x| < 2^E),  X_i = rint(x_i 2^(20-E)),  |X_i| <= 2^20,
+//   X = D0 + 128 D1 + 16384 D2  with balanced digits D0, D1 in [-64, 63], D2 in [-64, 64],
+// so that with q4_k weights y = d sc_j q - dmin m_j,
+//   sum_i x_i y_i ~= 2^(E-20) (d isum - dmin msum),
+//   isum = sum_t 128^t sum_i (sc q)_i D_t,i    three int8 MFMA accumulations per scale half, exact in int32,
+//   msum = sum_j m_j XS_j,  XS_j = sum_{i in j} X_i = P0 + 512 P1 + 2^18 P2 (f16-exact parts), one f16 MFMA
+// pair. The only rounding besides the 2^-21 grid is the fp32 epilogue, within the 1e-4 tolerance of the fast mode.
+// Rows holding NaN/Inf are computed with exact float dot products instead, as the act-quant path does.
+
+constexpr int FM_TM = 32, FM_TN = 128, FM_THREADS = 256;
+constexpr int FM_DIGIT = 8 * 1024;               // one digit plane of a 32-row block tile, MFMA lane order
+constexpr int FM_STAGE = 3 * FM_DIGIT + 2 * 1024 + FM_TM * 4;  // digits, msum A operands, exponents
+constexpr size_t FM_LDS = 2 * FM_STAGE + (FM_TM + 1) * sizeof(int);
+
+// Slot of 16-byte A piece (row r < 32, piece j < 16 of the block's 256 bytes) in a digit plane: chunk kc = j / 2
+// of 64 lanes, lane 32 (j % 2) + r, with the low four bits xor-ed by j so that the 16 pieces of one row (written
+// by 16 consecutive threads) fall on distinct LDS banks; the MFMA read of chunk kc by lane l is slot
+// 64 kc + (l ^ (2 kc + l / 32) % 16), a permutation of that chunk's 64 slots.
+__device__ __forceinline__ int fm_slot(int r, int j) { return 64 * (j >> 1) + ((32 * (j & 1) + r) ^ (j & 15)); }
+
+// One wave per (row m, block b): exponent, digit planes, the f16 parts of the sub-block sums, and a NaN/Inf flag.
+__global__ __launch_bounds__(256) void digits_q4k_kernel(const float *__restrict__ x, int64_t M, int64_t K,
+                                                         int8_t *__restrict__ dg, int *__restrict__ ex,
+                                                         uint16_t *__restrict__ xsp, uint8_t *__restrict__ bad) {
+    const int lane = threadIdx.x & 63;
+    const int64_t nb = K / 256;
+    const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (gw >= M * nb) return;  // wave-uniform
+    const int64_t m = gw / nb, b = gw % nb;
+    const float4 v = reinterpret_cast<const float4 *>(x + m * K + 256 * b)[lane];
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    const bool fin = (fabsf(v.x) <= FLT_MAX) && (fabsf(v.y) <= FLT_MAX) && (fabsf(v.z) <= FLT_MAX) &&
+                     (fabsf(v.w) <= FLT_MAX);
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    const bool allfin = __all(fin);
+    int E = 0;
+    if (allfin && amax > 0.0f) frexpf(amax, &E);
+    const float xv[4] = {v.x, v.y, v.z, v.w};
+    int X[4];
+    uint32_t d0 = 0, d1 = 0, d2 = 0;
+    int xs = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        X[i] = allfin ? (int)rintf(ldexpf(xv[i], 20 - E)) : 0;
+        const int a0 = ((X[i] + 64) & 127) - 64, r1 = (X[i] - a0) >> 7;
+        const int a1 = ((r1 + 64) & 127) - 64, a2 = (r1 - a1) >> 7;
+        d0 |= (uint32_t)(a0 & 0xFF) << (8 * i);
+        d1 |= (uint32_t)(a1 & 0xFF) << (8 * i);
+        d2 |= (uint32_t)(a2 & 0xFF) << (8 * i);
+        xs += X[i];
+    }
+    uint32_t *row = reinterpret_cast<uint32_t *>(dg + m * K + 256 * b) + lane;
+    const int64_t plane = M * K / 4;  // words per digit plane
+    row[0] = d0;
+    row[plane] = d1;
+    row[2 * plane] = d2;
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) xs += __shfl_xor(xs, o);  // sub-block j = lane / 8
+    if ((lane & 7) == 0) {
+        const int j = lane >> 3;
+        const int p0 = ((xs + 256) & 511) - 256, r = (xs - p0) >> 9;
+        const int p1 = ((r + 256) & 511) - 256, p2 = (r - p1) >> 9;
+        uint16_t *o = xsp + (m * nb + b) * 24;
+        o[j] = __builtin_bit_cast(uint16_t, (_Float16)(float)p0);
+        o[8 + j] = __builtin_bit_cast(uint16_t, (_Float16)(float)p1);
+        o[16 + j] = __builtin_bit_cast(uint16_t, (_Float16)(float)p2);
+    }
+    if (lane == 0) {
+        ex[m * nb + b] = E - 20;
+        bad[m * nb + b] = allfin ? 0 : 1;
+    }
+}
+
+// Workgroup (tile, slice): 32 activation rows x 128 weight rows over blocks [bps s, bps s + bps). Wave w owns weight
+// rows 32 w .. +31 (lane l: row l % 32, as in actq_mfma_q4k). A block's digit planes, msum operands and exponents
+// are staged in LDS (double-buffered, coalesced: 16 consecutive threads read one row's 256 bytes).
+template <bool ACC>
+__global__ __launch_bounds__(FM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void fastm_mfma_q4k(
+    const Planes p, int64_t N, int64_t row0, int64_t M, int64_t K, const float *__restrict__ x,
+    const int8_t *__restrict__ dg, const int *__restrict__ ex, const uint16_t *__restrict__ xsp,
+    const uint8_t *__restrict__ bad, int64_t bps, float *__restrict__ c, float *__restrict__ partial) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    int *rowbad = reinterpret_cast<int *>(lds + 2 * FM_STAGE);  // [FM_TM] 0 ok, 1 NaN/Inf row, 2 outside M
+    int *anybad = rowbad + FM_TM;
+    const int nb = (int)p.nb;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int64_t tmi, tni;
+    tile_of(blockIdx.x, (M + FM_TM - 1) / FM_TM, (N + FM_TN - 1) / FM_TN, tmi, tni);
+    const int64_t n0 = tni * FM_TN, m0 = tmi * FM_TM;
+    const int b0 = (int)(blockIdx.y * bps), b1 = (int)((blockIdx.y + 1) * bps < nb ? (blockIdx.y + 1) * bps : nb);
+    tile_row_flags<FM_TM, FM_THREADS>(bad, m0, M, nb, rowbad, anybad);
+
+    // staging roles: digit pieces P = tid + 256 i (i < 2) of each plane: row P / 16, piece P % 16; threads < 128 also
+    // stage one msum operand piece (row tid % 32, part pair tid / 32 < 2 ... see below), threads < 32 one exponent
+    const int64_t plane = M * K;
+    int8_t const *dsrc[2];
+    int dslot[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int P = tid + 256 * i, r = P >> 4, j = P & 15;
+        const int64_t gm = m0 + r < M ? m0 + r : M - 1;
+        dsrc[i] = dg + gm * K + 16 * j;
+        dslot[i] = fm_slot(r, j);
+    }
+    // msum A operands, 32x32x16 f16 layout (lane l: row l % 32, k 8 (l / 32) .. +7): operand 0 = [P0 | P1],
+    // operand 1 = [P2 | 0]; thread tid < 128 stages 16 bytes: operand tid / 64, lane tid % 64
+    const int sr = tid & 31, sop = (tid >> 6) & 1, shalf = (tid >> 5) & 1;
+    const int64_t sgm = m0 + sr < M ? m0 + sr : M - 1;
+    const uint16_t *ssrc = xsp + sgm * nb * 24 + 8 * (2 * sop + shalf);  // + 24 b; part 3 (sop 1, half 1) is zero
+    const int64_t egm = m0 + (tid & 31) < M ? m0 + (tid & 31) : M - 1;
+    v4i sa[2][3];
+    v4i ss = (v4i){0};
+    int se = 0;
+    auto fetch_a = [&](int b) {
+#pragma unroll
+        for (int t = 0; t < 3; t++)
+#pragma unroll
+            for (int i = 0; i < 2; i++) sa[i][t] = *reinterpret_cast<const v4i *>(dsrc[i] + t * plane + 256 * (int64_t)b);
+        if (tid < 128) ss = (sop == 1 && shalf == 1) ? (v4i){0} : *reinterpret_cast<const v4i *>(ssrc + 24 * (int64_t)b);
+        if (tid < FM_TM) se = ex[egm * nb + b];
+    };
+    auto put_a = [&](int buf) {
+        uint8_t *st = lds + buf * FM_STAGE;
+#pragma unroll
+        for (int t = 0; t < 3; t++)
+#pragma unroll
+            for (int i = 0; i < 2; i++) reinterpret_cast<v4i *>(st + t * FM_DIGIT)[dslot[i]] = sa[i][t];
+        if (tid < 128) reinterpret_cast<v4i *>(st + 3 * FM_DIGIT)[tid] = ss;
+        if (tid < FM_TM) reinterpret_cast<int *>(st + 3 * FM_DIGIT + 2048)[tid] = se;
+    };
+
+    const int nloc = 32 * w + (lane & 31);
+    const int64_t wrow = row0 + ((n0 + nloc) < N ? (n0 + nloc) : N - 1);
+    const uint4 *hq = reinterpret_cast<const uint4 *>(p.aux) + wrow * nb;
+    const uint4 *qq = reinterpret_cast<const uint4 *>(p.qs) + wrow * nb * 8 + 4 * (lane >> 5);
+    uint4 wh, wq[4];
+    auto fetch_w = [&](int b) {
+        wh = hq[b];
+#pragma unroll
+        for (int g = 0; g < 4; g++) wq[g] = qq[8 * b + g];
+    };
+
+    float accf[16];
+#pragma unroll
+    for (int v = 0; v < 16; v++) accf[v] = 0.0f;
+    if (b0 < b1) {
+        fetch_a(b0);
+        fetch_w(b0);
+        put_a(0);
+        if (b0 + 1 < b1) fetch_a(b0 + 1);
+    }
+    __syncthreads();
+
+    for (int b = b0; b < b1; b++) {
+        const uint8_t *st = lds + ((b - b0) & 1) * FM_STAGE;
+        uint32_t sc_lo, sc_hi, m_lo, m_hi;
+        q4k_scales(wh.y, wh.z, wh.w, sc_lo, sc_hi, m_lo, m_hi);
+        const float dd = f16_to_f32((uint16_t)(wh.x & 0xFFFF)), dm = f16_to_f32((uint16_t)(wh.x >> 16));
+        const uint4 cq[4] = {wq[0], wq[1], wq[2], wq[3]};
+        const uint32_t mlo = m_lo, mhi = m_hi;
+        if (b + 1 < b1) fetch_w(b + 1);
+
+        v16i c0[3], c1[3];
+#pragma unroll
+        for (int t = 0; t < 3; t++) {
+            c0[t] = (v16i){0};
+            c1[t] = (v16i){0};
+        }
+#pragma unroll
+        for (int kc = 0; kc < 8; kc++) {
+            const uint4 raw = cq[kc >> 1];
+            const uint4 nib = (kc & 1) ? make_uint4((raw.x >> 4) & 0x0F0F0F0Fu, (raw.y >> 4) & 0x0F0F0F0Fu,
+                                                    (raw.z >> 4) & 0x0F0F0F0Fu, (raw.w >> 4) & 0x0F0F0F0Fu)
+                                       : make_uint4(raw.x & 0x0F0F0F0Fu, raw.y & 0x0F0F0F0Fu, raw.z & 0x0F0F0F0Fu,
+                                                    raw.w & 0x0F0F0F0Fu);
+            const uint32_t sc = ((kc < 4 ? sc_lo : sc_hi) >> (8 * (kc & 3))) & 0xFF;
+            const v4i wb0 = mul16(nib, sc & 7), wb1 = mul16(nib, sc >> 3);
+            const int slot = 64 * kc + (lane ^ ((2 * kc + (lane >> 5)) & 15));
+#pragma unroll
+            for (int t = 0; t < 3; t++) {
+                const v4i a = reinterpret_cast<const v4i *>(st + t * FM_DIGIT)[slot];
+                c0[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, wb0, c0[t], 0, 0, 0);
+                c1[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, wb1, c1[t], 0, 0, 0);
+            }
+        }
+        float fs[16];  // sum_t 128^t isum_t
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const float f0 = (float)(c0[0][v] + 8 * c1[0][v]), f1 = (float)(c0[1][v] + 8 * c1[1][v]),
+                        f2 = (float)(c0[2][v] + 8 * c1[2][v]);
+            fs[v] = fmaf(16384.0f, f2, fmaf(128.0f, f1, f0));
+        }
+        if (b + 1 < b1) {
+            put_a((b + 1 - b0) & 1);
+            if (b + 2 < b1) fetch_a(b + 2);
+        }
+        // msum B operands of this lane's weight row: [m_0..7 | 512 m_0..7] and [m_0..7 | 0]
+        const uint32_t mul = (lane >> 5) ? 512u : 1u;
+        const v8h bm0 = __builtin_bit_cast(
+            v8h, make_uint4(pack_h2(mul * (mlo & 0xFF), mul * ((mlo >> 8) & 0xFF)),
+                            pack_h2(mul * ((mlo >> 16) & 0xFF), mul * (mlo >> 24)),
+                            pack_h2(mul * (mhi & 0xFF), mul * ((mhi >> 8) & 0xFF)),
+                            pack_h2(mul * ((mhi >> 16) & 0xFF), mul * (mhi >> 24))));
+        const v8h bm1 = (lane >> 5) ? (v8h){0, 0, 0, 0, 0, 0, 0, 0}
+                                    : __builtin_bit_cast(v8h, make_uint4(pack_h2(mlo & 0xFF, (mlo >> 8) & 0xFF),
+                                                                         pack_h2((mlo >> 16) & 0xFF, mlo >> 24),
+                                                                         pack_h2(mhi & 0xFF, (mhi >> 8) & 0xFF),
+                                                                         pack_h2((mhi >> 16) & 0xFF, mhi >> 24)));
+        const v8h am0 = *reinterpret_cast<const v8h *>(st + 3 * FM_DIGIT + 16 * lane);
+        const v8h am1 = *reinterpret_cast<const v8h *>(st + 3 * FM_DIGIT + 1024 + 16 * lane);
+        const v16f cm0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(am0, bm0, (v16f){0}, 0, 0, 0);
+        const v16f cm1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(am1, bm1, (v16f){0}, 0, 0, 0);
+        const int *exs = reinterpret_cast<const int *>(st + 3 * FM_DIGIT + 2048);
+#pragma unroll
+        for (int v4 = 0; v4 < 4; v4++) {
+            const int4 e4 = *reinterpret_cast<const int4 *>(exs + 8 * v4 + 4 * (lane >> 5));
+            const int ev[4] = {e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int v = 4 * v4 + r;
+                const float ms = fmaf(262144.0f, cm1[v], cm0[v]);
+                accf[v] = accf[v] + ldexpf(fmaf(dd, fs[v], -(dm * ms)), ev[r]);
+            }
+        }
+        __syncthreads();  // block b + 1 staged; nobody reads buffer (b - b0) & 1 any more
+    }
+
+    const int64_t gn = n0 + nloc;
+    float *dst = partial ? partial + (int64_t)blockIdx.y * M * N : c;
+    const bool acc_c = ACC && partial == nullptr;
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+        const int mloc = 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        if (gn < N && rowbad[mloc] == 0) {
+            float *o = dst + (m0 + mloc) * N + gn;
+            *o = acc_c ? *o + accf[v] : accf[v];
+        }
+    }
+    // rows holding NaN/Inf: exact float dot products over the whole row, by slice 0 (the other slices add zero)
+    if (!*anybad) return;
+    for (int i = tid; i < FM_TM * FM_TN; i += FM_THREADS) {
+        const int ml = i / FM_TN, nl = i % FM_TN;
+        const int64_t gn2 = n0 + nl;
+        if (rowbad[ml] != 1 || gn2 >= N) continue;
+        const int64_t gm = m0 + ml;
+        const float v = blockIdx.y == 0 ? exact_dot_row<kQ4K>(p, row0 + gn2, x + gm * K, K) : 0.0f;
+        float *o = dst + gm * N + gn2;
+        *o = acc_c ? *o + v : v;
+    }
+}
+
+// c[i] (+)= partial[0][i] + partial[1][i] + ... in slice order.
+template <bool ACC>
+__global__ void fm_sum_kernel(const float *__restrict__ partial, float *__restrict__ c, int64_t MN, int64_t ns) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < MN; i += (int64_t)gridDim.x * blockDim.x) {
+        float s = partial[i];
+        int64_t k = 1;
+        for (; k + 8 <= ns; k += 8) {  // eight loads in flight, added in slice order
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = partial[(k + u) * MN + i];
+#pragma unroll
+            for (int u = 0; u < 8; u++) s = s + v[u];
+        }
+        for (; k < ns; k++) s = s + partial[k * MN + i];
+        c[i] = ACC ? c[i] + s : s;
+    }
+}
+
 }  // namespace
 
 int launch_actq_mfma(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
@@ -285,6 +574,71 @@ int launch_actq_mfma(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_
     }();
     if (tm == 32) return run_mfma<32>(ctx, w, row0, N, x, c, M, acc, q, d, sj, bad);
     return run_mfma<64>(ctx, w, row0, N, x, c, M, acc, q, d, sj, bad);
+}
+
+}  // namespace trhip
+
+namespace trhip {
+
+// Fast-mode M > 1 for q4_k (tolerance 1e-4): digit planes of x, then the int8 MFMA kernel over K slices.
+int launch_gemm_rows_fast(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
+                          int64_t M, bool acc) {
+    if (w->dtype != kQ4K) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemm_rows_fast: q4_k only");
+    const int64_t K = w->K, nb = K / 256;
+    const int64_t tiles = ((N + FM_TN - 1) / FM_TN) * ((M + FM_TM - 1) / FM_TM);
+    int64_t ns = (512 + tiles - 1) / tiles;  // K slices for about 512 workgroups
+    if (ns > nb) ns = nb;
+    const int64_t bps = (nb + ns - 1) / ns;
+    ns = (nb + bps - 1) / bps;
+    auto al = [](size_t v) { return (v + 255) / 256 * 256; };
+    const bool copy_x = reinterpret_cast<uintptr_t>(x) % 16 != 0;
+    const size_t o_dg = 0, o_ex = al(o_dg + 3 * (size_t)(M * K)), o_xs = al(o_ex + (size_t)(M * nb) * sizeof(int));
+    const size_t o_bad = al(o_xs + (size_t)(M * nb) * 48), o_x = al(o_bad + (size_t)(M * nb));
+    const size_t o_p = al(o_x + (copy_x ? (size_t)(M * K) * sizeof(float) : 0));
+    const size_t total = o_p + (ns > 1 ? (size_t)(ns * M * N) * sizeof(float) : 0);
+    int st = TRHIP_OK;
+    uint8_t *ws = static_cast<uint8_t *>(workspace(ctx, total, &st));
+    if (!ws) return st;
+    const float *xa = x;
+    if (copy_x) {
+        hipError_t e = hipMemcpyAsync(ws + o_x, x, (size_t)(M * K) * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "gemm_rows_fast: align x");
+        xa = reinterpret_cast<const float *>(ws + o_x);
+    }
+    uint8_t *bad = ws + o_bad;
+    hipLaunchKernelGGL(digits_q4k_kernel, dim3((unsigned)((M * nb + 3) / 4)), dim3(256), 0, ctx->stream, xa, M, K,
+                       reinterpret_cast<int8_t *>(ws + o_dg), reinterpret_cast<int *>(ws + o_ex),
+                       reinterpret_cast<uint16_t *>(ws + o_xs), bad);
+    if ((st = launch_check(ctx, "digits_q4k")) != TRHIP_OK) return st;
+    static bool lds_set = false;
+    if (!lds_set) {
+        hipError_t e1 = hipFuncSetAttribute(reinterpret_cast<const void *>(&fastm_mfma_q4k<true>),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)FM_LDS);
+        hipError_t e2 = hipFuncSetAttribute(reinterpret_cast<const void *>(&fastm_mfma_q4k<false>),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)FM_LDS);
+        if (e1 != hipSuccess) return hip_fail(ctx, e1, "fastm_mfma: LDS size");
+        if (e2 != hipSuccess) return hip_fail(ctx, e2, "fastm_mfma: LDS size");
+        lds_set = true;
+    }
+    float *partial = ns > 1 ? reinterpret_cast<float *>(ws + o_p) : nullptr;
+    dim3 grid((unsigned)tiles, (unsigned)ns), block(FM_THREADS);
+    const int8_t *dg = reinterpret_cast<const int8_t *>(ws + o_dg);
+    const int *ex = reinterpret_cast<const int *>(ws + o_ex);
+    const uint16_t *xs = reinterpret_cast<const uint16_t *>(ws + o_xs);
+    if (acc && !partial)
+        hipLaunchKernelGGL(fastm_mfma_q4k<true>, grid, block, FM_LDS, ctx->stream, w->planes(), N, row0, M, K, xa, dg,
+                           ex, xs, bad, bps, c, partial);
+    else
+        hipLaunchKernelGGL(fastm_mfma_q4k<false>, grid, block, FM_LDS, ctx->stream, w->planes(), N, row0, M, K, xa, dg,
+                           ex, xs, bad, bps, c, partial);
+    if ((st = launch_check(ctx, "fastm_mfma_q4k")) != TRHIP_OK || !partial) return st;
+    const int64_t MN = M * N;
+    const unsigned blocks = (unsigned)((MN + 255) / 256 < 4096 ? (MN + 255) / 256 : 4096);
+    if (acc)
+        hipLaunchKernelGGL(fm_sum_kernel<true>, dim3(blocks), dim3(256), 0, ctx->stream, partial, c, MN, ns);
+    else
+        hipLaunchKernelGGL(fm_sum_kernel<false>, dim3(blocks), dim3(256), 0, ctx->stream, partial, c, MN, ns);
+    return launch_check(ctx, "fm_sum");
 }
 
 }  // namespace trhip

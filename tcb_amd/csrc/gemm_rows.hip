@@ -453,7 +453,15 @@ __global__ void sum_chunks_kernel(const float *__restrict__ partial, float *__re
                                   int64_t nchunks) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < MN; i += (int64_t)gridDim.x * blockDim.x) {
         float part = 0.0f;
-        for (int64_t ch = 0; ch < nchunks; ch++) part = part + partial[ch * MN + i];
+        int64_t ch = 0;
+        for (; ch + 8 <= nchunks; ch += 8) {  // eight loads in flight, added in chunk order
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = partial[(ch + u) * MN + i];
+#pragma unroll
+            for (int u = 0; u < 8; u++) part = part + v[u];
+        }
+        for (; ch < nchunks; ch++) part = part + partial[ch * MN + i];
         c[i] = ACC ? c[i] + part : part;
     }
 }

@@ -183,6 +183,8 @@ int launch_gemv(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, 
                 bool acc, int mode);
 int launch_gemm_rows(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                      int64_t M, bool acc);
+int launch_gemm_rows_fast(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
+                          int64_t M, bool acc);
 int launch_quantize_q8(trhip_ctx *ctx, const float *x, int64_t M, int64_t K, int blk, int8_t *q, float *d,
                        int16_t *bs, uint8_t *bad, uint16_t *sj);
 int launch_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
