@@ -255,6 +255,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl_q4k(const Planes p, const 
                                                           float *__restrict__ c, int64_t N, int64_t row0) {
     constexpr int RG = WAVES / KS;
     static_assert(16 % RG == 0, "the row groups of a part split the 16 columns of x evenly");
+    static_assert(RPW % PD == 0, "rows are consumed PD at a time from a ring of PD slots");
     constexpr int CPW = 16 / RG;
     __shared__ float part_lds[2][KS > 1 ? (KS - 1) * RG * 8 : 1];
     __shared__ uint32_t xd_lds[KS][16][3][64];
