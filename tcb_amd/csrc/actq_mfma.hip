@@ -31,6 +31,7 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int TN = 128, THREADS = 256;
 // Per row-tile height TM (64 or 32): LDS staging of one block, in MFMA lane order.
@@ -544,20 +545,236 @@ __global__ __launch_bounds__(FM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
     }
 }
 
+// The same for at most 16 activation rows, on 16-row tiles: v_mfma_i32_16x16x64_i8 and v_mfma_f32_16x16x32_f16
+// (lane l: row / column l % 16, k-slice l / 16 of 16 bytes / 8 halves; result register v of lane l: row 4 (l / 16) + v,
+// column l % 16, both checked on the device). Wave w owns weight rows 32 w .. +31 as two 16-column tiles; for 64-wide
+// chunk c of a block, lane l's B operand is elements 16 (l / 16) .. +15 of chunk c, i.e. of sub-block 2 c + l / 32,
+// held in the lane-sliced q4_k bytes 64 ((l / 16) & 1) + 16 c .. +15 (low nibbles for l < 32, high for l >= 32).
+constexpr int F16_TM = 16;
+constexpr int F16_DIGIT = 4 * 1024;                              // one digit plane of a 16-row block tile
+constexpr int F16_STAGE = 3 * F16_DIGIT + 2 * 1024 + F16_TM * 4;  // digits, msum A operands, exponents
+constexpr size_t F16_LDS = 2 * F16_STAGE + (F16_TM + 1) * sizeof(int);
+
+// Slot of 16-byte A piece (row r < 16, piece j < 16) in a 16-row digit plane: chunk j / 4 of 64 lanes, lane
+// 16 (j % 4) + r, low four bits xor-ed by j (the 16 pieces of a row land on distinct banks); the read of chunk c by
+// lane l is slot 64 c + (l ^ (4 c + l / 16) % 16).
+__device__ __forceinline__ int f16_slot(int r, int j) { return 64 * (j >> 2) + ((16 * (j & 3) + r) ^ (j & 15)); }
+
+template <bool ACC>
+__global__ __launch_bounds__(FM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void fastm16_mfma_q4k(
+    const Planes p, int64_t N, int64_t row0, int64_t M, int64_t K, const float *__restrict__ x,
+    const int8_t *__restrict__ dg, const int *__restrict__ ex, const uint16_t *__restrict__ xsp,
+    const uint8_t *__restrict__ bad, int64_t bps, float *__restrict__ c, float *__restrict__ partial) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    int *rowbad = reinterpret_cast<int *>(lds + 2 * F16_STAGE);
+    int *anybad = rowbad + F16_TM;
+    const int nb = (int)p.nb;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int64_t tmi, tni;
+    tile_of(blockIdx.x, (M + F16_TM - 1) / F16_TM, (N + FM_TN - 1) / FM_TN, tmi, tni);
+    const int64_t n0 = tni * FM_TN, m0 = tmi * F16_TM;
+    const int b0 = (int)(blockIdx.y * bps), b1 = (int)((blockIdx.y + 1) * bps < nb ? (blockIdx.y + 1) * bps : nb);
+    tile_row_flags<F16_TM, FM_THREADS>(bad, m0, M, nb, rowbad, anybad);
+
+    // staging: digit piece tid of each plane (row tid / 16, piece tid % 16); threads < 128 one msum operand piece
+    // (operand tid / 64: [P0 | P1 | 0 | 0] or [P2 | 0 | 0 | 0], lane tid % 64: row lane % 16, k-group lane / 16);
+    // threads < 16 one exponent
+    const int64_t plane = M * K;
+    const int dr = tid >> 4, dj = tid & 15;
+    const int8_t *dsrc = dg + (m0 + dr < M ? m0 + dr : M - 1) * K + 16 * dj;
+    const int dslot = f16_slot(dr, dj);
+    const int sl = tid & 63, sop = (tid >> 6) & 1, sgrp = sl >> 4;  // k-group of 8 halves
+    const int64_t sgm = m0 + (sl & 15) < M ? m0 + (sl & 15) : M - 1;
+    const bool sval = sop == 0 ? sgrp < 2 : sgrp == 0;  // which groups carry parts
+    const uint16_t *ssrc = xsp + sgm * nb * 24 + 8 * (sop == 0 ? sgrp : 2);  // + 24 b
+    const int64_t egm = m0 + (tid & 15) < M ? m0 + (tid & 15) : M - 1;
+    v4i sa[3];
+    v4i ss = (v4i){0};
+    int se = 0;
+    auto fetch_a = [&](int b) {
+#pragma unroll
+        for (int t = 0; t < 3; t++) sa[t] = *reinterpret_cast<const v4i *>(dsrc + t * plane + 256 * (int64_t)b);
+        if (tid < 128) ss = sval ? *reinterpret_cast<const v4i *>(ssrc + 24 * (int64_t)b) : (v4i){0};
+        if (tid < F16_TM) se = ex[egm * nb + b];
+    };
+    auto put_a = [&](int buf) {
+        uint8_t *st = lds + buf * F16_STAGE;
+#pragma unroll
+        for (int t = 0; t < 3; t++) reinterpret_cast<v4i *>(st + t * F16_DIGIT)[dslot] = sa[t];
+        if (tid < 128) reinterpret_cast<v4i *>(st + 3 * F16_DIGIT)[tid] = ss;
+        if (tid < F16_TM) reinterpret_cast<int *>(st + 3 * F16_DIGIT + 2048)[tid] = se;
+    };
+
+    // weights: lane l, tile t: row 32 w + 16 t + l % 16, bytes 64 ((l / 16) & 1) .. +63 of each block
+    const uint4 *hq[2], *qq[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        const int nl = 32 * w + 16 * t + (lane & 15);
+        const int64_t wrow = row0 + ((n0 + nl) < N ? (n0 + nl) : N - 1);
+        hq[t] = reinterpret_cast<const uint4 *>(p.aux) + wrow * nb;
+        qq[t] = reinterpret_cast<const uint4 *>(p.qs) + wrow * nb * 8 + 4 * ((lane >> 4) & 1);
+    }
+    uint4 wh[2], wq[2][4];
+    auto fetch_w = [&](int b) {
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            wh[t] = hq[t][b];
+#pragma unroll
+            for (int g = 0; g < 4; g++) wq[t][g] = qq[t][8 * b + g];
+        }
+    };
+
+    float accf[2][4];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) accf[t][v] = 0.0f;
+    if (b0 < b1) {
+        fetch_a(b0);
+        fetch_w(b0);
+        put_a(0);
+        if (b0 + 1 < b1) fetch_a(b0 + 1);
+    }
+    __syncthreads();
+
+    const int hi = lane >> 5;  // this lane's sub-blocks are 2 c + hi: high nibbles for hi = 1
+    for (int b = b0; b < b1; b++) {
+        const uint8_t *st = lds + ((b - b0) & 1) * F16_STAGE;
+        uint32_t scv[2][4];  // scale byte of sub-block 2 c + hi, per tile and chunk
+        uint32_t mv[2][2];   // the tile rows' m_0..7 (lo, hi words)
+        float dd[2], dm[2];
+        uint4 cq[2][4];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            uint32_t sc_lo, sc_hi, m_lo, m_hi;
+            q4k_scales(wh[t].y, wh[t].z, wh[t].w, sc_lo, sc_hi, m_lo, m_hi);
+            dd[t] = f16_to_f32((uint16_t)(wh[t].x & 0xFFFF));
+            dm[t] = f16_to_f32((uint16_t)(wh[t].x >> 16));
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++) {
+                const int j = 2 * cc + hi;
+                scv[t][cc] = ((j < 4 ? sc_lo : sc_hi) >> (8 * (j & 3))) & 0xFF;
+            }
+            mv[t][0] = m_lo;
+            mv[t][1] = m_hi;
+#pragma unroll
+            for (int g = 0; g < 4; g++) cq[t][g] = wq[t][g];
+        }
+        if (b + 1 < b1) fetch_w(b + 1);
+
+        v4i c0[2][3], c1[2][3];
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int d = 0; d < 3; d++) {
+                c0[t][d] = (v4i){0, 0, 0, 0};
+                c1[t][d] = (v4i){0, 0, 0, 0};
+            }
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++) {
+            const int slot = 64 * cc + (lane ^ ((4 * cc + (lane >> 4)) & 15));
+            v4i a[3];
+#pragma unroll
+            for (int d = 0; d < 3; d++) a[d] = reinterpret_cast<const v4i *>(st + d * F16_DIGIT)[slot];
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const uint4 raw = cq[t][cc];
+                const uint4 nib = hi ? make_uint4((raw.x >> 4) & 0x0F0F0F0Fu, (raw.y >> 4) & 0x0F0F0F0Fu,
+                                                  (raw.z >> 4) & 0x0F0F0F0Fu, (raw.w >> 4) & 0x0F0F0F0Fu)
+                                     : make_uint4(raw.x & 0x0F0F0F0Fu, raw.y & 0x0F0F0F0Fu, raw.z & 0x0F0F0F0Fu,
+                                                  raw.w & 0x0F0F0F0Fu);
+                const uint32_t sc = scv[t][cc];
+                const v4i wb0 = mul16(nib, sc & 7), wb1 = mul16(nib, sc >> 3);
+#pragma unroll
+                for (int d = 0; d < 3; d++) {
+                    c0[t][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[d], wb0, c0[t][d], 0, 0, 0);
+                    c1[t][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[d], wb1, c1[t][d], 0, 0, 0);
+                }
+            }
+        }
+        float fs[2][4];
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const float f0 = (float)(c0[t][0][v] + 8 * c1[t][0][v]), f1 = (float)(c0[t][1][v] + 8 * c1[t][1][v]),
+                            f2 = (float)(c0[t][2][v] + 8 * c1[t][2][v]);
+                fs[t][v] = fmaf(16384.0f, f2, fmaf(128.0f, f1, f0));
+            }
+        if (b + 1 < b1) {
+            put_a((b + 1 - b0) & 1);
+            if (b + 2 < b1) fetch_a(b + 2);
+        }
+        // msum: A operands [P0 | P1 | 0 | 0] and [P2 | 0 | 0 | 0] (k-groups of 8); B of this lane's column,
+        // k-group l / 16: [m_0..7 | 512 m_0..7 | 0 | 0] and [m_0..7 | 0 | 0 | 0]
+        const v8h am0 = *reinterpret_cast<const v8h *>(st + 3 * F16_DIGIT + 16 * lane);
+        const v8h am1 = *reinterpret_cast<const v8h *>(st + 3 * F16_DIGIT + 1024 + 16 * lane);
+        const int grp = lane >> 4;
+        const int *exs = reinterpret_cast<const int *>(st + 3 * F16_DIGIT + 2048);
+        const int4 e4 = *reinterpret_cast<const int4 *>(exs + 4 * grp);
+        const int ev[4] = {e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const uint32_t mlo = mv[t][0], mhi = mv[t][1];
+            const uint32_t mul = grp == 1 ? 512u : 1u;
+            const v8h mj = __builtin_bit_cast(
+                v8h, make_uint4(pack_h2(mul * (mlo & 0xFF), mul * ((mlo >> 8) & 0xFF)),
+                                pack_h2(mul * ((mlo >> 16) & 0xFF), mul * (mlo >> 24)),
+                                pack_h2(mul * (mhi & 0xFF), mul * ((mhi >> 8) & 0xFF)),
+                                pack_h2(mul * ((mhi >> 16) & 0xFF), mul * (mhi >> 24))));
+            const v8h zero = (v8h){0, 0, 0, 0, 0, 0, 0, 0};
+            const v8h bm0 = grp < 2 ? mj : zero, bm1 = grp == 0 ? mj : zero;
+            const v4f cm0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(am0, bm0, (v4f){0, 0, 0, 0}, 0, 0, 0);
+            const v4f cm1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(am1, bm1, (v4f){0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const float ms = fmaf(262144.0f, cm1[v], cm0[v]);
+                accf[t][v] = accf[t][v] + ldexpf(fmaf(dd[t], fs[t][v], -(dm[t] * ms)), ev[v]);
+            }
+        }
+        __syncthreads();
+    }
+
+    float *dst = partial ? partial + (int64_t)blockIdx.y * M * N : c;
+    const bool acc_c = ACC && partial == nullptr;
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        const int64_t gn = n0 + 32 * w + 16 * t + (lane & 15);
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int mloc = 4 * (lane >> 4) + v;
+            if (gn < N && rowbad[mloc] == 0) {
+                float *o = dst + (m0 + mloc) * N + gn;
+                *o = acc_c ? *o + accf[t][v] : accf[t][v];
+            }
+        }
+    }
+    if (!*anybad) return;
+    for (int i = tid; i < F16_TM * FM_TN; i += FM_THREADS) {
+        const int ml = i / FM_TN, nl = i % FM_TN;
+        const int64_t gn2 = n0 + nl;
+        if (rowbad[ml] != 1 || gn2 >= N) continue;
+        const int64_t gm = m0 + ml;
+        const float v = blockIdx.y == 0 ? exact_dot_row<kQ4K>(p, row0 + gn2, x + gm * K, K) : 0.0f;
+        float *o = dst + gm * N + gn2;
+        *o = acc_c ? *o + v : v;
+    }
+}
+
 // c[i] (+)= partial[0][i] + partial[1][i] + ... in slice order.
 template <bool ACC>
 __global__ void fm_sum_kernel(const float *__restrict__ partial, float *__restrict__ c, int64_t MN, int64_t ns) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < MN; i += (int64_t)gridDim.x * blockDim.x) {
         float s = partial[i];
-        int64_t k = 1;
-        for (; k + 8 <= ns; k += 8) {  // eight loads in flight, added in slice order
+        for (int64_t k = 1; k < ns; k += 8) {  // up to eight loads in flight, added in slice order
             float v[8];
 #pragma unroll
-            for (int u = 0; u < 8; u++) v[u] = partial[(k + u) * MN + i];
+            for (int u = 0; u < 8; u++) v[u] = k + u < ns ? partial[(k + u) * MN + i] : 0.0f;
 #pragma unroll
-            for (int u = 0; u < 8; u++) s = s + v[u];
+            for (int u = 0; u < 8; u++)
+                if (k + u < ns) s = s + v[u];
         }
-        for (; k < ns; k++) s = s + partial[k * MN + i];
         c[i] = ACC ? c[i] + s : s;
     }
 }
@@ -585,7 +802,8 @@ int launch_gemm_rows_fast(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, i
                           int64_t M, bool acc) {
     if (w->dtype != kQ4K) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemm_rows_fast: q4_k only");
     const int64_t K = w->K, nb = K / 256;
-    const int64_t tiles = ((N + FM_TN - 1) / FM_TN) * ((M + FM_TM - 1) / FM_TM);
+    const bool t16 = M <= F16_TM;  // one 16-row tile
+    const int64_t tiles = ((N + FM_TN - 1) / FM_TN) * (t16 ? 1 : (M + FM_TM - 1) / FM_TM);
     int64_t ns = (512 + tiles - 1) / tiles;  // K slices for about 512 workgroups
     if (ns > nb) ns = nb;
     const int64_t bps = (nb + ns - 1) / ns;
@@ -610,27 +828,27 @@ int launch_gemm_rows_fast(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, i
                        reinterpret_cast<int8_t *>(ws + o_dg), reinterpret_cast<int *>(ws + o_ex),
                        reinterpret_cast<uint16_t *>(ws + o_xs), bad);
     if ((st = launch_check(ctx, "digits_q4k")) != TRHIP_OK) return st;
-    static bool lds_set = false;
-    if (!lds_set) {
-        hipError_t e1 = hipFuncSetAttribute(reinterpret_cast<const void *>(&fastm_mfma_q4k<true>),
-                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)FM_LDS);
-        hipError_t e2 = hipFuncSetAttribute(reinterpret_cast<const void *>(&fastm_mfma_q4k<false>),
-                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)FM_LDS);
-        if (e1 != hipSuccess) return hip_fail(ctx, e1, "fastm_mfma: LDS size");
-        if (e2 != hipSuccess) return hip_fail(ctx, e2, "fastm_mfma: LDS size");
-        lds_set = true;
-    }
     float *partial = ns > 1 ? reinterpret_cast<float *>(ws + o_p) : nullptr;
     dim3 grid((unsigned)tiles, (unsigned)ns), block(FM_THREADS);
     const int8_t *dg = reinterpret_cast<const int8_t *>(ws + o_dg);
     const int *ex = reinterpret_cast<const int *>(ws + o_ex);
     const uint16_t *xs = reinterpret_cast<const uint16_t *>(ws + o_xs);
-    if (acc && !partial)
-        hipLaunchKernelGGL(fastm_mfma_q4k<true>, grid, block, FM_LDS, ctx->stream, w->planes(), N, row0, M, K, xa, dg,
-                           ex, xs, bad, bps, c, partial);
-    else
-        hipLaunchKernelGGL(fastm_mfma_q4k<false>, grid, block, FM_LDS, ctx->stream, w->planes(), N, row0, M, K, xa, dg,
-                           ex, xs, bad, bps, c, partial);
+    const bool acc_k = acc && !partial;
+    if (t16) {  // LDS below 64 KB: no attribute needed
+        if (acc_k)
+            hipLaunchKernelGGL(fastm16_mfma_q4k<true>, grid, block, F16_LDS, ctx->stream, w->planes(), N, row0, M, K,
+                               xa, dg, ex, xs, bad, bps, c, partial);
+        else
+            hipLaunchKernelGGL(fastm16_mfma_q4k<false>, grid, block, F16_LDS, ctx->stream, w->planes(), N, row0, M, K,
+                               xa, dg, ex, xs, bad, bps, c, partial);
+    } else {
+        if (acc_k)
+            hipLaunchKernelGGL(fastm_mfma_q4k<true>, grid, block, FM_LDS, ctx->stream, w->planes(), N, row0, M, K, xa,
+                               dg, ex, xs, bad, bps, c, partial);
+        else
+            hipLaunchKernelGGL(fastm_mfma_q4k<false>, grid, block, FM_LDS, ctx->stream, w->planes(), N, row0, M, K, xa,
+                               dg, ex, xs, bad, bps, c, partial);
+    }
     if ((st = launch_check(ctx, "fastm_mfma_q4k")) != TRHIP_OK || !partial) return st;
     const int64_t MN = M * N;
     const unsigned blocks = (unsigned)((MN + 255) / 256 < 4096 ? (MN + 255) / 256 : 4096);

@@ -453,15 +453,14 @@ __global__ void sum_chunks_kernel(const float *__restrict__ partial, float *__re
                                   int64_t nchunks) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < MN; i += (int64_t)gridDim.x * blockDim.x) {
         float part = 0.0f;
-        int64_t ch = 0;
-        for (; ch + 8 <= nchunks; ch += 8) {  // eight loads in flight, added in chunk order
+        for (int64_t ch = 0; ch < nchunks; ch += 8) {  // up to eight loads in flight, added in chunk order
             float v[8];
 #pragma unroll
-            for (int u = 0; u < 8; u++) v[u] = partial[(ch + u) * MN + i];
+            for (int u = 0; u < 8; u++) v[u] = ch + u < nchunks ? partial[(ch + u) * MN + i] : 0.0f;
 #pragma unroll
-            for (int u = 0; u < 8; u++) part = part + v[u];
+            for (int u = 0; u < 8; u++)
+                if (ch + u < nchunks) part = part + v[u];
         }
-        for (; ch < nchunks; ch++) part = part + partial[ch * MN + i];
         c[i] = ACC ? c[i] + part : part;
     }
 }
