@@ -784,11 +784,15 @@ __global__ void fm_sum_kernel(const float *__restrict__ partial, float *__restri
 int launch_actq_mfma(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                      int64_t M, bool acc, const int8_t *q, const float *d, const uint16_t *sj, const uint8_t *bad) {
     if (w->dtype != kQ4K) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "actq_mfma: q4_k only");
-    // row-tile height: TRHIP_ACTQ_TM (32 or 64) overrides the default
-    static const int tm = [] {
+    // Row-tile height: 64 rows unless that leaves fewer than 160 workgroups (measured: 4096 x 14336 at M = 128
+    // takes 74 us on 32-row tiles against 104 on 64; 14336 x 4096 at M = 128 or 512 is faster on 64).
+    // TRHIP_ACTQ_TM (32 or 64) overrides.
+    static const int tm_env = [] {
         const char *e = getenv("TRHIP_ACTQ_TM");
-        return (e && atoi(e) == 32) ? 32 : 64;
+        return e ? atoi(e) : 0;
     }();
+    const int64_t wgs64 = ((N + TN - 1) / TN) * ((M + 63) / 64);
+    const int tm = tm_env == 32 || tm_env == 64 ? tm_env : (wgs64 < 160 ? 32 : 64);
     if (tm == 32) return run_mfma<32>(ctx, w, row0, N, x, c, M, acc, q, d, sj, bad);
     return run_mfma<64>(ctx, w, row0, N, x, c, M, acc, q, d, sj, bad);
 }
