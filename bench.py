@@ -15,9 +15,10 @@ restatement of the reference's sdotq4k path (oracle/trq_avx2.c), all host cores,
 
 Prints one JSON line. --gpus N > 1 exits: this build runs on one GPU.
 
---profile-kernel {gemv,prefill,copy} runs only that kernel, eagerly, --steps times (for rocprofv3 counter runs):
-gemv = the headline GEMV over the cold ring, prefill = one act-quant GEMM per step, copy = a plain device copy of
-COPY_BYTES (torch) that calibrates the FETCH_SIZE / WRITE_SIZE counters.
+--profile-kernel {gemv,prefill,rows,copy} runs only that kernel, eagerly, --steps times (for rocprofv3 runs):
+gemv = the headline GEMV over the cold ring, prefill = one act-quant GEMM per step, rows = one M > 1 fp32 GEMM
+(--rows-m rows, --mode exact or fast) per step, copy = a plain device copy of COPY_BYTES (torch) that calibrates
+the FETCH_SIZE / WRITE_SIZE counters.
 """
 import argparse
 import json
@@ -62,8 +63,9 @@ def parse():
     ap.add_argument("--sweep", type=int, default=1, help="also time the 32-layer decode sweep (0 = skip)")
     ap.add_argument("--shapes", type=int, default=1,
                     help="also time every Llama-3-8B GEMV shape per dtype and the prefill grid (0 = skip)")
-    ap.add_argument("--profile-kernel", choices=["gemv", "prefill", "copy"], default=None,
+    ap.add_argument("--profile-kernel", choices=["gemv", "prefill", "rows", "copy"], default=None,
                     help="run only this kernel --steps times, eagerly (counter runs)")
+    ap.add_argument("--rows-m", type=int, default=16, help="activation rows of --profile-kernel rows (M > 1 path)")
     return ap.parse_args()
 
 
@@ -231,6 +233,18 @@ def profile_kernel(a):
         tb.ctx.sync()
         print(json.dumps({"profiled": "gemv_q4_k_%s" % a.mode, "launches": a.steps,
                           "algorithmic_bytes": algorithmic_bytes(N, K)}))
+    elif a.profile_kernel == "rows":
+        # the M > 1 fp32 path (batched decode): exact chunk order, or the fast int8-digit kernel with --mode fast
+        M = a.rows_m
+        w = tb.FromQuantized(Q4K, raw, N, K)
+        Xb = tb.ctx.to_device(synth.activations(M, K, seed=5))
+        Cb = tb.ctx.alloc(M * N * 4)
+        mode = MODE_FAST if a.mode == "fast" else MODE_EXACT
+        for _ in range(a.steps):
+            tb.GemmSet(M, N, K, Xb, w, Cb, mode=mode)
+        tb.ctx.sync()
+        print(json.dumps({"profiled": "rows_q4_k_%s" % a.mode, "launches": a.steps, "M": M,
+                          "algorithmic_bytes": algorithmic_bytes(N, K) + 4 * (M - 1) * (N + K)}))
     else:
         M = a.prefill_m
         w = tb.FromQuantized(Q4K, raw, N, K)
