@@ -20,25 +20,38 @@
 namespace trhip {
 namespace {
 
-// Stage n float4 of x into LDS with `threads` threads: all loads of a batch are issued before any
-// store so the L2 round trips overlap.
+// Stage n float4 of x into LDS with THREADS threads, a batch of U float4 per thread at a time. issue() requests a
+// batch (clamped, unconditional loads); commit() stores it. The empty asm on every loaded value keeps the loads
+// ahead of it: without it the compiler moves each load into its store's branch, and a wait follows each one.
+// A kernel issues the first batch, then its weight loads, then commits, so x and the first weights are in
+// flight together and the wait before the stores covers x only.
 template <int THREADS>
-__device__ __forceinline__ void stage_x(float4 *xs, const float4 *__restrict__ x4, int64_t n) {
-    constexpr int U = 8;
-    for (int64_t i0 = 0; i0 < n; i0 += (int64_t)U * THREADS) {
-        float4 v[U];
-#pragma unroll
-        for (int u = 0; u < U; u++) {  // clamped, unconditional loads keep v[] in registers
-            int64_t i = i0 + (int64_t)u * THREADS + threadIdx.x;
-            v[u] = x4[i < n ? i : n - 1];
-        }
+struct XStager {
+    static constexpr int U = 8;
+    float4 v[U];
+    __device__ __forceinline__ void issue(const float4 *__restrict__ x4, int64_t n, int64_t i0) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            int64_t i = i0 + (int64_t)u * THREADS + threadIdx.x;
+            const int64_t i = i0 + (int64_t)u * THREADS + threadIdx.x;
+            v[u] = x4[i < n ? i : n - 1];
+        }
+    }
+    __device__ __forceinline__ void commit(float4 *xs, int64_t n, int64_t i0) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            asm volatile("" : "+v"(v[u].x), "+v"(v[u].y), "+v"(v[u].z), "+v"(v[u].w));
+            const int64_t i = i0 + (int64_t)u * THREADS + threadIdx.x;
             if (i < n) xs[i] = v[u];
         }
     }
-}
+    // the batches after the first
+    __device__ __forceinline__ void rest(float4 *xs, const float4 *__restrict__ x4, int64_t n) {
+        for (int64_t i0 = (int64_t)U * THREADS; i0 < n; i0 += (int64_t)U * THREADS) {
+            issue(x4, n, i0);
+            commit(xs, n, i0);
+        }
+    }
+};
 
 __device__ __forceinline__ void fma4(float *acc, uint32_t codes, float s, float negm, float4 xv) {
     codes = opaque(codes);
@@ -208,10 +221,14 @@ __global__ __launch_bounds__(THREADS) void gemv_exact_kernel(const Planes p, con
     constexpr int D = B::DEPTH;
     B blk(p, row, t);
     typename B::Data ring[D];
-    // weights first (they come from HBM), then x into LDS
+    // x (cache-resident) and the first weight blocks (from HBM) in flight together, then x into LDS
+    XStager<THREADS> xst;
+    xst.issue(reinterpret_cast<const float4 *>(x), K / 4, 0);
+    __builtin_amdgcn_sched_barrier(0);  // x is requested first: the wait before its stores then skips the weights
 #pragma unroll
     for (int s = 0; s < D; s++) blk.load(ring[s], s < nb ? s : nb - 1);
-    stage_x<THREADS>(xs, reinterpret_cast<const float4 *>(x), K / 4);
+    xst.commit(xs, K / 4, 0);
+    xst.rest(xs, reinterpret_cast<const float4 *>(x), K / 4);
     __syncthreads();
 
     float acc[8];
@@ -376,9 +393,13 @@ __global__ __launch_bounds__(THREADS) void gemv_exact8_kernel(const Planes p, co
     constexpr int D = B::DEPTH;
     B blk(p, row, u);
     typename B::Data ring[D];
+    XStager<THREADS> xst;
+    xst.issue(reinterpret_cast<const float4 *>(x), K / 4, 0);
+    __builtin_amdgcn_sched_barrier(0);  // x is requested first: the wait before its stores then skips the weights
 #pragma unroll
     for (int s = 0; s < D; s++) blk.load(ring[s], s < nb ? s : nb - 1);
-    stage_x<THREADS>(xs, reinterpret_cast<const float4 *>(x), K / 4);
+    xst.commit(xs, K / 4, 0);
+    xst.rest(xs, reinterpret_cast<const float4 *>(x), K / 4);
     __syncthreads();
 
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
