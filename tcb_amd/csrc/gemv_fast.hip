@@ -463,9 +463,12 @@ int launch_gemv_fast(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_
             }
             return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv_kl: no such launch shape");
         }
-        // Measured on cold 1.1 GiB rings (us): 14336 x 4096 8.6-8.9 K across lanes vs 11.6-12.2 row-sliced;
-        // at 4096 or fewer rows, or K > 4096, the row-sliced kernel below is faster.
-        if (N >= 8192 && w->nb >= 8 && w->nb <= 16) return run_kl<4, 1, 4, 16>(ctx, w, row0, N, x, c, acc);
+        // Measured on cold 1.1 GiB rings (us), K = 4096: 14336 rows 8.6 K across lanes (16 rows per wave) vs
+        // 11.6-12.2 row-sliced, 28672 rows 14.7 vs 15.9 with 8 rows per wave; 6144 / 8192 rows 5.6 / 5.8 with 8 rows
+        // per wave vs 7.9 / 8.0 with 16 and 6.2-6.5 / 8.0 row-sliced; at 4096 or fewer rows, or K > 4096, the
+        // row-sliced kernel below is faster.
+        if (N >= 10240 && w->nb >= 8 && w->nb <= 16) return run_kl<4, 1, 4, 16>(ctx, w, row0, N, x, c, acc);
+        if (N >= 6144 && w->nb >= 8 && w->nb <= 16) return run_kl<4, 1, 4, 8>(ctx, w, row0, N, x, c, acc);
         // launch shape "D,WAVES,KS,R": blocks in flight per lane, waves per workgroup, K parts per row group,
         // rows per lane. Measured on cold 1.1 GiB rings: splitting K wins while the grid is small (1024 / 4096 rows
         // at K = 4096: 5.5 / 5.9 us with 2 parts vs 7.9 / 8.2 whole), whole rows per wave win from ~8192 rows

@@ -433,9 +433,10 @@ def test_gemv_fast_tolerance(backend, dt, N, K):
     w.release()
 
 
-@pytest.mark.parametrize("N,K", LLAMA_LINEARS)
+@pytest.mark.parametrize("N,K", LLAMA_LINEARS + [(6144, 4096), (7000, 4096), (28672, 4096)])
 def test_gemv_fast_llama_shapes(backend, N, K):
-    """The fast q4_k GEMV on every Llama-3-8B linear shape (encoded weights with 1% outliers) within 1e-4."""
+    """The fast q4_k GEMV on every Llama-3-8B linear shape and the merged [q | k | v] (6144) and [gate | up] (28672)
+    stores, plus a ragged 7000 rows (encoded weights with 1% outliers), within 1e-4."""
     raw = synth.quant_weights(Q4K, N, K, seed=51, outliers=0.01)
     x = synth.activations(1, K, seed=52)
     w = backend.FromQuantized(Q4K, raw, N, K)
