@@ -250,9 +250,34 @@ __device__ __forceinline__ void x4_digits(const float *xv, int e, uint32_t out[3
 // (its own, cached) and are not stored. With KS > 1 the parts 1..KS-1 hand their row sums through LDS to
 // part 0, which adds them in part order. The RG row groups of a part share x: each loads and digitizes 16 / RG
 // of the 16 four-element columns, through LDS. Weights are requested PD rows ahead, after x.
-template <bool ACC, int WAVES, int KS, int PD, int RPW>
-__global__ __launch_bounds__(64 * WAVES) void gemv_kl_q4k(const Planes p, const float *__restrict__ x,
-                                                          float *__restrict__ c, int64_t N, int64_t row0) {
+//
+// q8_0 / q4_0 (32-element blocks, y = d*q and y = d*(q - 8), tensor/quant.go:139-155) use the same lanes, x
+// digits and row streaming: lane l owns blocks 2l and 2l + 1 of its part (up to 128 blocks), which are the same
+// 64 contiguous elements, one block per 32-element half. q8_0: the codes are signed bytes, four per v_dot4;
+// q4_0: byte j of a block holds elements j (low nibble) and j + 16 (high nibble), so the low nibbles meet digit
+// words 0..3 of the half and the high nibbles words 4..7. Per block, sum_e y_e x_e = d * 2^(e-22) * sum_e q_e X_e
+// (q8_0) or d * (2^(e-22) * sum_e q_e X_e - 8 * sum_e x_e) (q4_0).
+template <int DT>
+struct KlRow;  // one row slot: the bytes a lane reads for its 64 elements
+
+template <>
+struct KlRow<kQ4K> {
+    uint4 h, q0, q1;
+};
+template <>
+struct KlRow<kQ8> {
+    uint4 q[4];
+    uint32_t d;  // the two blocks' fp16 scales
+};
+template <>
+struct KlRow<kQ4> {
+    uint4 q0, q1;
+    uint32_t d;
+};
+
+template <int DT, bool ACC, int WAVES, int KS, int PD, int RPW>
+__global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const float *__restrict__ x,
+                                                      float *__restrict__ c, int64_t N, int64_t row0) {
     constexpr int RG = WAVES / KS;
     static_assert(16 % RG == 0, "the row groups of a part split the 16 columns of x evenly");
     static_assert(RPW % PD == 0, "rows are consumed PD at a time from a ring of PD slots");
@@ -264,33 +289,51 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl_q4k(const Planes p, const 
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int rg = w / KS, part = w % KS;
     const int nb = (int)p.nb;
-    const int bpp = (nb + KS - 1) / KS;
+    constexpr bool K4 = DT == kQ4K;
+    // blocks per part (even for q8_0 / q4_0: the launcher requires an even block count)
+    const int bpp = K4 ? (nb + KS - 1) / KS : ((nb + KS - 1) / KS + 1) / 2 * 2;
     const int pb0 = part * bpp, pb1 = pb0 + bpp < nb ? pb0 + bpp : nb;
-    const int g = lane & 3, b = pb0 + (lane >> 2);
+    const int g = lane & 3, b = pb0 + (K4 ? (lane >> 2) : 2 * lane);
     const bool active = b < pb1;
-    const int bc = active ? b : (pb0 < nb ? pb0 : nb - 1);  // inactive lanes read a valid block, add nothing
-    const float4 *x4 = reinterpret_cast<const float4 *>(x + 256 * (int64_t)bc + 64 * g);
+    const int bc = active ? b : (pb0 < nb ? pb0 : (K4 ? nb - 1 : nb - 2));  // inactive lanes read valid blocks
+    const float4 *x4 = reinterpret_cast<const float4 *>(x + (K4 ? 256 * (int64_t)bc + 64 * g : 32 * (int64_t)bc));
     // issue order: this wave's columns of x (cache-resident), then the first PD rows, so that waiting for x
     // leaves the rows in flight
     float4 xraw[CPW];
 #pragma unroll
     for (int i = 0; i < CPW; i++) xraw[i] = x4[rg * CPW + i];
     const int k0 = (2 * g) & 3, k1 = k0 + 1;
+    // q4_k: header of the lane's block, and qs 16-byte pieces g and g + 4 of it; q8_0 / q4_0: the two blocks'
+    // codes (64 / 32 contiguous bytes) and their two fp16 scales (one aligned dword)
     const uint4 *hb = reinterpret_cast<const uint4 *>(p.aux) + bc;
-    const uint4 *qb = reinterpret_cast<const uint4 *>(p.qs) + 8 * (int64_t)bc + g;  // + 4: bytes 16 .. 31
+    const uint4 *qb = reinterpret_cast<const uint4 *>(p.qs) +
+                      (K4 ? 8 * (int64_t)bc + g : (DT == kQ8 ? 2 * (int64_t)bc : (int64_t)bc));
+    const uint32_t *db = reinterpret_cast<const uint32_t *>(p.d) + bc / 2;
+    constexpr int QW = K4 ? 8 : (DT == kQ8 ? 2 * 32 / 16 * 2 : 32 / 16);  // uint4 per row in the qs plane / (nb)
+    auto load_row = [&](KlRow<DT> &rw, int64_t row) {
+        if constexpr (K4) {
+            rw.h = hb[row * nb];
+            rw.q0 = qb[row * nb * 8];
+            rw.q1 = qb[row * nb * 8 + 4];
+        } else if constexpr (DT == kQ8) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) rw.q[i] = qb[row * nb * 2 + i];
+            rw.d = db[row * (nb / 2)];
+        } else {
+            rw.q0 = qb[row * nb];
+            rw.q1 = qb[row * nb + 1];
+            rw.d = db[row * (nb / 2)];
+        }
+    };
+    (void)QW;
     // row counts fit 32 bits (the launcher checks), so the uniform row arithmetic stays 32-bit
     const uint32_t G = gridDim.x * RG, gw = blockIdx.x * RG + rg, n32 = (uint32_t)N;
     const uint32_t nv = gw < n32 ? (n32 - 1 - gw) / G + 1 : 0;                 // rows of this row group
     const uint32_t last = nv > 0 ? gw + (nv - 1) * G : gw - (gw / n32) * n32;  // what slots past them re-read
     auto row_of = [&](int i) { return row0 + (int64_t)((uint32_t)i < nv ? gw + (uint32_t)i * G : last); };
-    uint4 H[PD], Q0[PD], Q1[PD];
+    KlRow<DT> R[PD];
 #pragma unroll
-    for (int s = 0; s < PD; s++) {
-        const int64_t row = row_of(s);
-        H[s] = hb[row * nb];
-        Q0[s] = qb[row * nb * 8];
-        Q1[s] = qb[row * nb * 8 + 4];
-    }
+    for (int s = 0; s < PD; s++) load_row(R[s], row_of(s));
     __builtin_amdgcn_sched_barrier(0);
     // per-wave partial sums and maxima of its columns' halves meet in LDS (added in wave order); then each wave
     // turns its columns into digits for all 64 lanes, which every wave of the part reads back
@@ -348,7 +391,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl_q4k(const Planes p, const 
 #pragma unroll
         for (int s = 0; s < 8; s++) {
             const int slot = s % PD;
-            const uint4 h = H[slot], q0 = Q0[slot], q1 = Q1[slot];
+            const KlRow<DT> rw = R[slot];
+            float a;
+            if constexpr (K4) {
+            const uint4 h = rw.h, q0 = rw.q0, q1 = rw.q1;
             const float d = f16_to_f32((uint16_t)(h.x & 0xFFFF)), dmin = f16_to_f32((uint16_t)(h.x >> 16));
             uint32_t sc_lo, sc_hi, m_lo, m_hi;
             q4k_scales(h.y, h.z, h.w, sc_lo, sc_hi, m_lo, m_hi);
@@ -370,7 +416,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl_q4k(const Planes p, const 
             // |l1| * 256 + |l0| < 2^24: the first two digits add exactly
             const float pl = fmaf((float)l2, 65536.0f, fmaf((float)l1, 256.0f, (float)l0));
             const float ph = fmaf((float)h2, 65536.0f, fmaf((float)h1, 256.0f, (float)h0));
-            float a = ldexpf(s0 * pl, ex[0]);
+            a = ldexpf(s0 * pl, ex[0]);
             a = fmaf(n0, sxl, a);
             a = a + ldexpf(s1 * ph, ex[1]);
             a = fmaf(n1, sxh, a);
@@ -388,13 +434,73 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl_q4k(const Planes p, const 
                     }
                 }
             }
-            v[s] = active ? a : 0.0f;
-            if (i0 + s + PD < RPW) {  // refill the slot just consumed
-                const int64_t row = row_of(i0 + s + PD);
-                H[slot] = hb[row * nb];
-                Q0[slot] = qb[row * nb * 8];
-                Q1[slot] = qb[row * nb * 8 + 4];
+            } else {
+            // q8_0: 16 code words, 8 per block; q4_0: 8 words, 4 per block (low nibbles then high nibbles)
+            const float d0 = f16_to_f32((uint16_t)(rw.d & 0xFFFF)), d1 = f16_to_f32((uint16_t)(rw.d >> 16));
+            int acc8[2][3] = {{0, 0, 0}, {0, 0, 0}};
+            uint32_t qw[16];
+            if constexpr (DT == kQ8) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    qw[4 * i] = rw.q[i].x;
+                    qw[4 * i + 1] = rw.q[i].y;
+                    qw[4 * i + 2] = rw.q[i].z;
+                    qw[4 * i + 3] = rw.q[i].w;
+                }
+#pragma unroll
+                for (int hf = 0; hf < 2; hf++)
+#pragma unroll
+                    for (int k = 0; k < 8; k++)
+#pragma unroll
+                        for (int t = 0; t < 3; t++)
+                            acc8[hf][t] = __builtin_amdgcn_sdot4((int)qw[8 * hf + k], xd[hf][k][t], acc8[hf][t], false);
+            } else {
+                const uint32_t w8[8] = {rw.q0.x, rw.q0.y, rw.q0.z, rw.q0.w, rw.q1.x, rw.q1.y, rw.q1.z, rw.q1.w};
+#pragma unroll
+                for (int hf = 0; hf < 2; hf++)
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        const uint32_t wd = w8[4 * hf + k];
+                        qw[8 * hf + k] = wd & 0x0F0F0F0Fu;             // elements 4k .. 4k+3
+                        qw[8 * hf + 4 + k] = (wd >> 4) & 0x0F0F0F0Fu;  // elements 16 + 4k ..
+                    }
+#pragma unroll
+                for (int hf = 0; hf < 2; hf++)
+#pragma unroll
+                    for (int k = 0; k < 8; k++)
+#pragma unroll
+                        for (int t = 0; t < 3; t++)
+                            acc8[hf][t] = __builtin_amdgcn_sdot4((int)qw[8 * hf + k], xd[hf][k][t], acc8[hf][t], false);
             }
+            const float pl = fmaf((float)acc8[0][2], 65536.0f, fmaf((float)acc8[0][1], 256.0f, (float)acc8[0][0]));
+            const float ph = fmaf((float)acc8[1][2], 65536.0f, fmaf((float)acc8[1][1], 256.0f, (float)acc8[1][0]));
+            if constexpr (DT == kQ8) {
+                a = d0 * ldexpf(pl, ex[0]) + d1 * ldexpf(ph, ex[1]);
+            } else {
+                a = d0 * fmaf(-8.0f, sxl, ldexpf(pl, ex[0])) + d1 * fmaf(-8.0f, sxh, ldexpf(ph, ex[1]));
+            }
+            if (!fin) {  // Inf or NaN in this lane's x: dequantized values times x in float
+                a = 0.0f;
+#pragma unroll
+                for (int hf = 0; hf < 2; hf++) {
+                    const float dd = hf ? d1 : d0;
+#pragma unroll
+                    for (int k = 0; k < 8; k++) {
+                        const float4 xv = x4[8 * hf + k];
+                        const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
+                        const uint32_t wq = qw[8 * hf + k];
+#pragma unroll
+                        for (int t = 0; t < 4; t++) {
+                            const float q = DT == kQ8 ? (float)(int8_t)((wq >> (8 * t)) & 0xFF)
+                                                      : ubyte_f(wq, t) - 8.0f;
+                            a = fmaf(dd * q, xs[t], a);  // fl(d*q) is exact for these codes
+                        }
+                    }
+                }
+            }
+            }
+            v[s] = active ? a : 0.0f;
+            if (i0 + s + PD < RPW) load_row(R[slot], row_of(i0 + s + PD));  // refill the slot just consumed
         }
         float sum = lane_sum8(v, lane);
         const int ri = lane >> 3;
@@ -412,19 +518,26 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl_q4k(const Planes p, const 
     }
 }
 
-template <int WAVES, int KS, int PD, int RPW>
+// Whether the K-across-lanes kernel takes a store with nb blocks per row in KS parts: q4_k parts of at most 16
+// blocks; q8_0 / q4_0 an even block count and parts of at most 128 blocks (two per lane).
+__host__ __forceinline__ bool kl_fits(int dt, int64_t nb, int ks) {
+    if (dt == kQ4K) return (nb + ks - 1) / ks <= 16;
+    return nb % 2 == 0 && ((nb + ks - 1) / ks + 1) / 2 * 2 <= 128;
+}
+
+template <int DT, int WAVES, int KS, int PD, int RPW>
 int run_kl(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c, bool acc) {
     constexpr int RG = WAVES / KS;
-    if ((w->nb + KS - 1) / KS > 16) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv_kl: K parts of more than 16 blocks");
+    if (!kl_fits(DT, w->nb, KS)) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv_kl: K parts of more than 16 blocks");
     const int64_t wgs = (N + RG * RPW - 1) / (RG * RPW);  // every row group gets at most RPW rows
     if (N >= (int64_t)1 << 31 || wgs * RG >= (int64_t)1 << 31)
         return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv_kl: more than 2^31 rows");
     dim3 grid((unsigned)wgs), block(64 * WAVES);
     if (acc)
-        hipLaunchKernelGGL((gemv_kl_q4k<true, WAVES, KS, PD, RPW>), grid, block, 0, ctx->stream, w->planes(), x, c, N, row0);
+        hipLaunchKernelGGL((gemv_kl<DT, true, WAVES, KS, PD, RPW>), grid, block, 0, ctx->stream, w->planes(), x, c, N, row0);
     else
-        hipLaunchKernelGGL((gemv_kl_q4k<false, WAVES, KS, PD, RPW>), grid, block, 0, ctx->stream, w->planes(), x, c, N, row0);
-    return launch_check(ctx, "gemv_kl_q4k");
+        hipLaunchKernelGGL((gemv_kl<DT, false, WAVES, KS, PD, RPW>), grid, block, 0, ctx->stream, w->planes(), x, c, N, row0);
+    return launch_check(ctx, "gemv_kl");
 }
 
 template <int D, int WAVES, int KS, int R>
@@ -446,29 +559,60 @@ int run_q4k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, cons
 int launch_gemv(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c, bool acc,
                 int mode);
 
+namespace {
+// K across lanes with the launch shape "WAVES,KS,PD,RPW" given in TRHIP_KL (read on every call, for tuning), or
+// kNotTaken when TRHIP_KL is not set.
+constexpr int kNotTaken = -1;
+template <int DT>
+int kl_forced(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c, bool acc) {
+    const char *kl = getenv("TRHIP_KL");
+    int wv = 0, ks = 0, pd = 0, rpw = 0;
+    if (!kl || sscanf(kl, "%d,%d,%d,%d", &wv, &ks, &pd, &rpw) != 4) return kNotTaken;
+    switch (10000 * wv + 1000 * ks + 10 * pd + rpw / 8) {
+    case 41041: return run_kl<DT, 4, 1, 4, 8>(ctx, w, row0, N, x, c, acc);
+    case 41042: return run_kl<DT, 4, 1, 4, 16>(ctx, w, row0, N, x, c, acc);
+    case 41022: return run_kl<DT, 4, 1, 2, 16>(ctx, w, row0, N, x, c, acc);
+    case 81041: return run_kl<DT, 8, 1, 4, 8>(ctx, w, row0, N, x, c, acc);
+    case 42042: return run_kl<DT, 4, 2, 4, 16>(ctx, w, row0, N, x, c, acc);
+    case 42041: return run_kl<DT, 4, 2, 4, 8>(ctx, w, row0, N, x, c, acc);
+    case 82041: return run_kl<DT, 8, 2, 4, 8>(ctx, w, row0, N, x, c, acc);
+    case 84041: return run_kl<DT, 8, 4, 4, 8>(ctx, w, row0, N, x, c, acc);
+    }
+    return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv_kl: no such launch shape");
+}
+
+// q8_0 / q4_0: K across lanes where the store fits it, else the exact kernel (within any tolerance)
+template <int DT>
+int kl_q8q4(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c, bool acc) {
+    const int f = kl_forced<DT>(ctx, w, row0, N, x, c, acc);
+    if (f != kNotTaken) return f;
+    // cold 1.1 GiB rings (us): q8_0 4096 x 4096 7.2 (one K part) / 6.9 (two), 14336 x 4096 12.7 with 16 rows per
+    // wave; q4_0 4096 x 4096 5.5 / 6.2, 14336 x 4096 8.2; K = 14336 takes four parts (q8_0 15.0, q4_0 10.7)
+    if (N < 10240 && DT == kQ8 && kl_fits(DT, w->nb, 2)) return run_kl<DT, 4, 2, 4, 8>(ctx, w, row0, N, x, c, acc);
+    if (kl_fits(DT, w->nb, 1)) {
+        if (N >= 10240) return run_kl<DT, 4, 1, 4, 16>(ctx, w, row0, N, x, c, acc);
+        return run_kl<DT, 4, 1, 4, 8>(ctx, w, row0, N, x, c, acc);
+    }
+    if (kl_fits(DT, w->nb, 4)) return run_kl<DT, 8, 4, 4, 8>(ctx, w, row0, N, x, c, acc);
+    return kNotTaken;
+}
+}  // namespace
+
 int launch_gemv_fast(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                      bool acc) {
+    if (w->dtype == kQ8 || w->dtype == kQ4) {
+        const int r = w->dtype == kQ8 ? kl_q8q4<kQ8>(ctx, w, row0, N, x, c, acc) : kl_q8q4<kQ4>(ctx, w, row0, N, x, c, acc);
+        if (r != kNotTaken) return r;
+    }
     if (w->dtype == kQ4K) {
-        // K across lanes: "WAVES,KS,PD,RPW" from TRHIP_KL (read on every call, for tuning) forces that kernel
-        const char *kl = getenv("TRHIP_KL");
-        int wv = 0, ks = 0, pd = 0, rpw = 0;
-        if (kl && sscanf(kl, "%d,%d,%d,%d", &wv, &ks, &pd, &rpw) == 4) {
-            switch (10000 * wv + 1000 * ks + 10 * pd + rpw / 8) {
-            case 41041: return run_kl<4, 1, 4, 8>(ctx, w, row0, N, x, c, acc);
-            case 41042: return run_kl<4, 1, 4, 16>(ctx, w, row0, N, x, c, acc);
-            case 41022: return run_kl<4, 1, 2, 16>(ctx, w, row0, N, x, c, acc);
-            case 81041: return run_kl<8, 1, 4, 8>(ctx, w, row0, N, x, c, acc);
-            case 42042: return run_kl<4, 2, 4, 16>(ctx, w, row0, N, x, c, acc);
-            case 84041: return run_kl<8, 4, 4, 8>(ctx, w, row0, N, x, c, acc);
-            }
-            return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv_kl: no such launch shape");
-        }
+        const int f = kl_forced<kQ4K>(ctx, w, row0, N, x, c, acc);
+        if (f != kNotTaken) return f;
         // Measured on cold 1.1 GiB rings (us), K = 4096: 14336 rows 8.6 K across lanes (16 rows per wave) vs
         // 11.6-12.2 row-sliced, 28672 rows 14.7 vs 15.9 with 8 rows per wave; 6144 / 8192 rows 5.6 / 5.8 with 8 rows
         // per wave vs 7.9 / 8.0 with 16 and 6.2-6.5 / 8.0 row-sliced; at 4096 or fewer rows, or K > 4096, the
         // row-sliced kernel below is faster.
-        if (N >= 10240 && w->nb >= 8 && w->nb <= 16) return run_kl<4, 1, 4, 16>(ctx, w, row0, N, x, c, acc);
-        if (N >= 6144 && w->nb >= 8 && w->nb <= 16) return run_kl<4, 1, 4, 8>(ctx, w, row0, N, x, c, acc);
+        if (N >= 10240 && w->nb >= 8 && w->nb <= 16) return run_kl<kQ4K, 4, 1, 4, 16>(ctx, w, row0, N, x, c, acc);
+        if (N >= 6144 && w->nb >= 8 && w->nb <= 16) return run_kl<kQ4K, 4, 1, 4, 8>(ctx, w, row0, N, x, c, acc);
         // launch shape "D,WAVES,KS,R": blocks in flight per lane, waves per workgroup, K parts per row group,
         // rows per lane. Measured on cold 1.1 GiB rings: splitting K wins while the grid is small (1024 / 4096 rows
         // at K = 4096: 5.5 / 5.9 us with 2 parts vs 7.9 / 8.2 whole), whole rows per wave win from ~8192 rows

@@ -770,3 +770,95 @@ def test_gemm_rows_fast_small_m_exact(backend):
     for b in (xb, cb):
         b.free()
     w.release()
+
+
+Q84_SHAPES = [(4096, 4096), (14336, 4096), (4096, 14336), (300, 1024), (77, 8192)]
+
+
+@pytest.mark.parametrize("dt", [Q8, Q4])
+@pytest.mark.parametrize("N,K", Q84_SHAPES)
+def test_gemv_fast_q8_q4(backend, dt, N, K):
+    """Fast q8_0 / q4_0 GEMV (K across lanes over fixed-point x) on the configs' shapes and ragged ones, set and
+    accumulate, x1 and x1000: within the 1e-5 bound."""
+    raw = synth.quant_weights(dt, N, K, seed=N + 3 * K)
+    w = backend.FromQuantized(dt, raw, N, K)
+    for scale, acc in ((1.0, False), (1000.0, True)):
+        x = synth.activations(1, K, seed=K + 7) * np.float32(scale)
+        c0 = synth.activations(1, N, seed=N + 1).reshape(-1)
+        xb, cb = backend.ctx.to_device(x), backend.ctx.to_device(c0)
+        if acc:
+            backend.Gemm(1, N, K, xb, w, cb, mode=MODE_FAST)
+        else:
+            backend.GemmSet(1, N, K, xb, w, cb, mode=MODE_FAST)
+        want = O.quant_gemm(dt, 1, N, K, x, raw, c0 if acc else None).reshape(-1)
+        err = rel_err(cb.download(np.float32, N) / scale, want / scale)
+        assert err <= FAST_TOL[dt], (dt, N, K, scale, err)
+        for b in (xb, cb):
+            b.free()
+    w.release()
+
+
+@pytest.mark.parametrize("dt", [Q8, Q4])
+@pytest.mark.parametrize("cfg", ["4,1,4,8", "4,1,4,16", "4,1,2,16", "8,1,4,8", "4,2,4,16", "4,2,4,8", "8,2,4,8",
+                                 "8,4,4,8"])
+def test_gemv_fast_q8_q4_launch_shapes(backend, monkeypatch, dt, cfg):
+    """Every launch shape of the K-across-lanes kernel for q8_0 / q4_0 on ragged rows and K parts (K = 8192 and
+    2560: parts of 128 and 40 blocks), within 1e-5; shapes whose parts exceed 128 blocks are refused."""
+    monkeypatch.setenv("TRHIP_KL", cfg)
+    ks = int(cfg.split(",")[1])
+    for N, K in ((133, 8192), (70, 2560)):
+        raw = synth.quant_weights(dt, N, K, seed=N + K)
+        w = backend.FromQuantized(dt, raw, N, K)
+        x = synth.activations(1, K, seed=K)
+        xb, cb = backend.ctx.to_device(x), backend.ctx.alloc(N * 4)
+        nb = K // 32
+        if ((nb + ks - 1) // ks + 1) // 2 * 2 > 128:
+            with pytest.raises(TrhipError) as e:
+                backend.GemmSet(1, N, K, xb, w, cb, mode=MODE_FAST)
+            assert e.value.code == 5
+        else:
+            backend.GemmSet(1, N, K, xb, w, cb, mode=MODE_FAST)
+            err = rel_err(cb.download(np.float32, N), O.quant_gemm(dt, 1, N, K, x, raw).reshape(-1))
+            assert err <= FAST_TOL[dt], (cfg, N, K, err)
+        for b in (xb, cb):
+            b.free()
+        w.release()
+
+
+@pytest.mark.parametrize("dt", [Q8, Q4])
+@pytest.mark.parametrize("bad", [np.inf, np.nan])
+def test_gemv_fast_q8_q4_non_finite(backend, dt, bad):
+    """Inf / NaN in x: float products in the lanes that hold it, NaN and +-Inf exactly where the exact GEMV has
+    them."""
+    N, K = 90, 4096
+    raw = synth.quant_weights(dt, N, K, seed=12)
+    w = backend.FromQuantized(dt, raw, N, K)
+    x = synth.activations(1, K, seed=13).reshape(-1)
+    x[1000] = bad
+    xb, cb = backend.ctx.to_device(x), backend.ctx.alloc(N * 4)
+    backend.GemmSet(1, N, K, xb, w, cb, mode=MODE_FAST)
+    got = cb.download(np.float32, N)
+    want = O.quant_gemm(dt, 1, N, K, x, raw).reshape(-1)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(np.isinf(got), np.isinf(want))
+    fin = np.isfinite(want)
+    assert np.array_equal(np.sign(got[~fin & ~np.isnan(want)]), np.sign(want[~fin & ~np.isnan(want)]))
+    for b in (xb, cb):
+        b.free()
+    w.release()
+
+
+@pytest.mark.parametrize("dt", [Q8, Q4])
+def test_gemv_fast_q8_q4_odd_blocks_exact(backend, dt):
+    """An odd number of 32-element blocks per row does not fit two blocks per lane: the fast mode runs the exact
+    kernel (same bits as mode exact)."""
+    N, K = 50, 32 * 9
+    raw = _weights(dt, N, K, 3)
+    w = backend.FromQuantized(dt, raw, N, K)
+    x = _x(_rng(4), K)
+    xb, cb = backend.ctx.to_device(x), backend.ctx.alloc(N * 4)
+    backend.GemmSet(1, N, K, xb, w, cb, mode=MODE_FAST)
+    same_bits(cb.download(np.float32, N), O.quant_gemm(dt, 1, N, K, x, raw).reshape(-1))
+    for b in (xb, cb):
+        b.free()
+    w.release()
