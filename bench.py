@@ -159,7 +159,7 @@ def decode_sweep(tb, batches, mode, replays=5):
 
 
 def shape_table(tb):
-    """Cold-ring GEMV time for every Llama-3-8B linear shape and dtype (exact, plus fast for q8_0 / q4_0 / q4_k), and the prefill
+    """Cold-ring GEMV time for every Llama-3-8B linear shape and dtype (exact and fast), and the prefill
     grid M in {128, 512, 2048} x both FFN shapes. Random-code blocks (synth.random_blocks): timing only."""
     from tcb_amd import MODE_EXACT, MODE_FAST, Q4, Q4K, Q6K, Q8, _lib, synth
     L = _lib.lib()
@@ -174,7 +174,7 @@ def shape_table(tb):
         xb = ctx.to_device(synth.activations(1, k, seed=6))
         cb = ctx.alloc(n * 4)
         res = {}
-        for md in ((MODE_EXACT, MODE_FAST) if dt in (Q8, Q4, Q4K) else (MODE_EXACT,)):
+        for md in (MODE_EXACT, MODE_FAST):
             tb.GemmSet(1, n, k, xb, ring[0], cb, mode=md)
             ctx.sync()
             g = capture(tb, lambda: [tb.GemmSet(1, n, k, xb, w, cb, mode=md) for w in ring])

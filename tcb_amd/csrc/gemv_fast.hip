@@ -274,6 +274,12 @@ struct KlRow<kQ4> {
     uint4 q0, q1;
     uint32_t d;
 };
+template <>
+struct KlRow<kQ6K> {  // ql pieces t at 32t + 16n, qh pieces at 16t + 8n, the lane's four scales, d
+    uint4 ql[4];
+    uint2 qh[4];
+    uint32_t sc, d;
+};
 
 template <int DT, bool ACC, int WAVES, int KS, int PD, int RPW>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const float *__restrict__ x,
@@ -289,7 +295,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const floa
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int rg = w / KS, part = w % KS;
     const int nb = (int)p.nb;
-    constexpr bool K4 = DT == kQ4K;
+    constexpr bool K4 = DT == kQ4K || DT == kQ6K;  // 256-element blocks, four lanes per block
     // blocks per part (even for q8_0 / q4_0: the launcher requires an even block count)
     const int bpp = K4 ? (nb + KS - 1) / KS : ((nb + KS - 1) / KS + 1) / 2 * 2;
     const int pb0 = part * bpp, pb1 = pb0 + bpp < nb ? pb0 + bpp : nb;
@@ -309,12 +315,27 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const floa
     const uint4 *qb = reinterpret_cast<const uint4 *>(p.qs) +
                       (K4 ? 8 * (int64_t)bc + g : (DT == kQ8 ? 2 * (int64_t)bc : (int64_t)bc));
     const uint32_t *db = reinterpret_cast<const uint32_t *>(p.d) + bc / 2;
+    // q6_k: elements 64g .. 64g+63 of the block are 32-element groups k4 = 2 (g & 1) and + 1 of half n = g >> 1;
+    // the repacked ql bytes of (t, k4 & 1, l) sit at 32t + 16n + 8 (k4 & 1) + l (low nibbles for k4 < 2), the qh
+    // bytes of (t, l) at 16t + 8n + l (bits 2 k4), the scales of the four 16-element quarters at 8n + 4 (g & 1)
+    const int n6 = g >> 1;
+    const uint4 *qlb = reinterpret_cast<const uint4 *>(p.qs) + 8 * (int64_t)bc + n6;
+    const uint2 *qhb = reinterpret_cast<const uint2 *>(p.aux) + 8 * (int64_t)bc + n6;
+    const uint32_t *scb = reinterpret_cast<const uint32_t *>(p.sc) + 4 * (int64_t)bc + 2 * n6 + (g & 1);
     constexpr int QW = K4 ? 8 : (DT == kQ8 ? 2 * 32 / 16 * 2 : 32 / 16);  // uint4 per row in the qs plane / (nb)
     auto load_row = [&](KlRow<DT> &rw, int64_t row) {
-        if constexpr (K4) {
+        if constexpr (DT == kQ4K) {
             rw.h = hb[row * nb];
             rw.q0 = qb[row * nb * 8];
             rw.q1 = qb[row * nb * 8 + 4];
+        } else if constexpr (DT == kQ6K) {
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                rw.ql[t] = qlb[row * nb * 8 + 2 * t];
+                rw.qh[t] = qhb[row * nb * 8 + 2 * t];
+            }
+            rw.sc = scb[row * nb * 4];
+            rw.d = p.d[row * nb + bc];
         } else if constexpr (DT == kQ8) {
 #pragma unroll
             for (int i = 0; i < 4; i++) rw.q[i] = qb[row * nb * 2 + i];
@@ -385,6 +406,19 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const floa
             for (int t = 0; t < 3; t++) xd[col >> 3][col & 7][t] = (int)xd_lds[part][col][t][lane];
     }
     const bool fin = __builtin_isfinite(sxl) && __builtin_isfinite(sxh);  // false also when a finite sum overflows
+    // q6_k: every 16-element quarter's chains start at -32 * (its digit sum), so that they hold sum (q - 32) X
+    int c6[4][3];
+    if constexpr (DT == kQ6K) {
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+            for (int t = 0; t < 3; t++) {
+                int sdg = 0;
+#pragma unroll
+                for (int k = 0; k < 4; k++) sdg = __builtin_amdgcn_sdot4(0x01010101, xd[q >> 1][4 * (q & 1) + k][t], sdg, false);
+                c6[q][t] = -32 * sdg;
+            }
+    }
 #pragma unroll
     for (int i0 = 0; i0 < RPW; i0 += 8) {
         float v[8];
@@ -393,7 +427,54 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const floa
             const int slot = s % PD;
             const KlRow<DT> rw = R[slot];
             float a;
-            if constexpr (K4) {
+            if constexpr (DT == kQ6K) {
+            const float d6 = f16_to_f32((uint16_t)(rw.d & 0xFFFF));
+            const int sh = 4 * (g & 1);  // this lane's nibble and its qh bit pair base
+            uint32_t code[2][8];  // [k4 & 1][word]: codes 0..63 of elements 4 word .. +3 of the group
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const uint32_t lw[4] = {rw.ql[t].x, rw.ql[t].y, rw.ql[t].z, rw.ql[t].w};
+                const uint32_t hw[2] = {rw.qh[t].x, rw.qh[t].y};
+#pragma unroll
+                for (int kk = 0; kk < 2; kk++)
+#pragma unroll
+                    for (int j = 0; j < 2; j++) {
+                        const uint32_t nib = (lw[2 * kk + j] >> sh) & 0x0F0F0F0Fu;
+                        const uint32_t hi2 = ((hw[j] >> (sh + 2 * kk)) & 0x03030303u) << 4;
+                        code[kk][2 * t + j] = nib | hi2;
+                    }
+            }
+            float pq[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                int l0 = c6[q][0], l1 = c6[q][1], l2 = c6[q][2];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int cw = (int)code[q >> 1][4 * (q & 1) + k];
+                    l0 = __builtin_amdgcn_sdot4(cw, xd[q >> 1][4 * (q & 1) + k][0], l0, false);
+                    l1 = __builtin_amdgcn_sdot4(cw, xd[q >> 1][4 * (q & 1) + k][1], l1, false);
+                    l2 = __builtin_amdgcn_sdot4(cw, xd[q >> 1][4 * (q & 1) + k][2], l2, false);
+                }
+                pq[q] = fmaf((float)l2, 65536.0f, fmaf((float)l1, 256.0f, (float)l0));
+            }
+            const float s0 = (float)(int8_t)(rw.sc & 0xFF), s1 = (float)(int8_t)((rw.sc >> 8) & 0xFF);
+            const float s2 = (float)(int8_t)((rw.sc >> 16) & 0xFF), s3 = (float)(int8_t)(rw.sc >> 24);
+            a = ldexpf(d6 * fmaf(s1, pq[1], s0 * pq[0]), ex[0]) + ldexpf(d6 * fmaf(s3, pq[3], s2 * pq[2]), ex[1]);
+            if (!fin) {  // Inf or NaN in this lane's x: dequantized values times x in float
+                a = 0.0f;
+#pragma unroll
+                for (int kk = 0; kk < 2; kk++)
+#pragma unroll
+                    for (int k = 0; k < 8; k++) {
+                        const float4 xv = x4[8 * kk + k];
+                        const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
+                        const float ds = d6 * (float)(int8_t)((rw.sc >> (8 * (2 * kk + (k >> 2)))) & 0xFF);
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            a = fmaf(ds * (ubyte_f(code[kk][k], e) - 32.0f), xs[e], a);  // fl(fl(d*sc)*(q-32))
+                    }
+            }
+            } else if constexpr (DT == kQ4K) {
             const uint4 h = rw.h, q0 = rw.q0, q1 = rw.q1;
             const float d = f16_to_f32((uint16_t)(h.x & 0xFFFF)), dmin = f16_to_f32((uint16_t)(h.x >> 16));
             uint32_t sc_lo, sc_hi, m_lo, m_hi;
@@ -518,17 +599,17 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const floa
     }
 }
 
-// Whether the K-across-lanes kernel takes a store with nb blocks per row in KS parts: q4_k parts of at most 16
-// blocks; q8_0 / q4_0 an even block count and parts of at most 128 blocks (two per lane).
+// Whether the K-across-lanes kernel takes a store with nb blocks per row in KS parts: q4_k / q6_k parts of at
+// most 16 blocks; q8_0 / q4_0 an even block count and parts of at most 128 blocks (two per lane).
 __host__ __forceinline__ bool kl_fits(int dt, int64_t nb, int ks) {
-    if (dt == kQ4K) return (nb + ks - 1) / ks <= 16;
+    if (dt == kQ4K || dt == kQ6K) return (nb + ks - 1) / ks <= 16;
     return nb % 2 == 0 && ((nb + ks - 1) / ks + 1) / 2 * 2 <= 128;
 }
 
 template <int DT, int WAVES, int KS, int PD, int RPW>
 int run_kl(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c, bool acc) {
     constexpr int RG = WAVES / KS;
-    if (!kl_fits(DT, w->nb, KS)) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv_kl: K parts of more than 16 blocks");
+    if (!kl_fits(DT, w->nb, KS)) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv_kl: K parts too long for the lanes of a wave");
     const int64_t wgs = (N + RG * RPW - 1) / (RG * RPW);  // every row group gets at most RPW rows
     if (N >= (int64_t)1 << 31 || wgs * RG >= (int64_t)1 << 31)
         return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv_kl: more than 2^31 rows");
@@ -596,10 +677,26 @@ int kl_q8q4(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, cons
     if (kl_fits(DT, w->nb, 4)) return run_kl<DT, 8, 4, 4, 8>(ctx, w, row0, N, x, c, acc);
     return kNotTaken;
 }
+
+// q6_k: K across lanes (K up to 4096 in one part, K up to 16384 in four), else the exact kernel
+int kl_q6k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c, bool acc) {
+    const int f = kl_forced<kQ6K>(ctx, w, row0, N, x, c, acc);
+    if (f != kNotTaken) return f;
+    if (kl_fits(kQ6K, w->nb, 1)) {
+        if (N >= 10240) return run_kl<kQ6K, 4, 1, 4, 16>(ctx, w, row0, N, x, c, acc);
+        return run_kl<kQ6K, 4, 1, 4, 8>(ctx, w, row0, N, x, c, acc);
+    }
+    if (kl_fits(kQ6K, w->nb, 4)) return run_kl<kQ6K, 8, 4, 4, 8>(ctx, w, row0, N, x, c, acc);
+    return kNotTaken;
+}
 }  // namespace
 
 int launch_gemv_fast(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                      bool acc) {
+    if (w->dtype == kQ6K) {
+        const int r = kl_q6k(ctx, w, row0, N, x, c, acc);
+        if (r != kNotTaken) return r;
+    }
     if (w->dtype == kQ8 || w->dtype == kQ4) {
         const int r = w->dtype == kQ8 ? kl_q8q4<kQ8>(ctx, w, row0, N, x, c, acc) : kl_q8q4<kQ4>(ctx, w, row0, N, x, c, acc);
         if (r != kNotTaken) return r;

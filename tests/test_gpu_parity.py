@@ -775,12 +775,12 @@ def test_gemm_rows_fast_small_m_exact(backend):
 Q84_SHAPES = [(4096, 4096), (14336, 4096), (4096, 14336), (300, 1024), (77, 8192)]
 
 
-@pytest.mark.parametrize("dt", [Q8, Q4])
+@pytest.mark.parametrize("dt", [Q8, Q4, Q6K])
 @pytest.mark.parametrize("N,K", Q84_SHAPES)
 def test_gemv_fast_q8_q4(backend, dt, N, K):
-    """Fast q8_0 / q4_0 GEMV (K across lanes over fixed-point x) on the configs' shapes and ragged ones, set and
-    accumulate, x1 and x1000: within the 1e-5 bound."""
-    raw = synth.quant_weights(dt, N, K, seed=N + 3 * K)
+    """Fast q8_0 / q4_0 / q6_k GEMV (K across lanes over fixed-point x) on the configs' shapes and ragged ones,
+    set and accumulate, x1 and x1000: within the 1e-5 (q8_0, q4_0) and 1e-4 (q6_k) bounds."""
+    raw = synth.quant_weights(dt, N, K, seed=N + 3 * K, outliers=0.01 if dt == Q6K else 0.0)
     w = backend.FromQuantized(dt, raw, N, K)
     for scale, acc in ((1.0, False), (1000.0, True)):
         x = synth.activations(1, K, seed=K + 7) * np.float32(scale)
@@ -798,21 +798,23 @@ def test_gemv_fast_q8_q4(backend, dt, N, K):
     w.release()
 
 
-@pytest.mark.parametrize("dt", [Q8, Q4])
+@pytest.mark.parametrize("dt", [Q8, Q4, Q6K])
 @pytest.mark.parametrize("cfg", ["4,1,4,8", "4,1,4,16", "4,1,2,16", "8,1,4,8", "4,2,4,16", "4,2,4,8", "8,2,4,8",
                                  "8,4,4,8"])
 def test_gemv_fast_q8_q4_launch_shapes(backend, monkeypatch, dt, cfg):
-    """Every launch shape of the K-across-lanes kernel for q8_0 / q4_0 on ragged rows and K parts (K = 8192 and
-    2560: parts of 128 and 40 blocks), within 1e-5; shapes whose parts exceed 128 blocks are refused."""
+    """Every launch shape of the K-across-lanes kernel for q8_0 / q4_0 / q6_k on ragged rows and K parts (K = 8192
+    and 2560: parts of up to 128 blocks of 32, or 16 of 256), within the bound; shapes whose parts exceed that are
+    refused."""
     monkeypatch.setenv("TRHIP_KL", cfg)
     ks = int(cfg.split(",")[1])
     for N, K in ((133, 8192), (70, 2560)):
-        raw = synth.quant_weights(dt, N, K, seed=N + K)
+        raw = synth.quant_weights(dt, N, K, seed=N + K, outliers=0.01 if dt == Q6K else 0.0)
         w = backend.FromQuantized(dt, raw, N, K)
         x = synth.activations(1, K, seed=K)
         xb, cb = backend.ctx.to_device(x), backend.ctx.alloc(N * 4)
-        nb = K // 32
-        if ((nb + ks - 1) // ks + 1) // 2 * 2 > 128:
+        nb = K // BLOCK[dt][0]
+        too_big = (nb + ks - 1) // ks > 16 if dt == Q6K else ((nb + ks - 1) // ks + 1) // 2 * 2 > 128
+        if too_big:
             with pytest.raises(TrhipError) as e:
                 backend.GemmSet(1, N, K, xb, w, cb, mode=MODE_FAST)
             assert e.value.code == 5
@@ -825,7 +827,7 @@ def test_gemv_fast_q8_q4_launch_shapes(backend, monkeypatch, dt, cfg):
         w.release()
 
 
-@pytest.mark.parametrize("dt", [Q8, Q4])
+@pytest.mark.parametrize("dt", [Q8, Q4, Q6K])
 @pytest.mark.parametrize("bad", [np.inf, np.nan])
 def test_gemv_fast_q8_q4_non_finite(backend, dt, bad):
     """Inf / NaN in x: float products in the lanes that hold it, NaN and +-Inf exactly where the exact GEMV has
