@@ -159,8 +159,9 @@ def decode_sweep(tb, batches, mode, replays=5):
 
 
 def shape_table(tb):
-    """Cold-ring GEMV time for every Llama-3-8B linear shape and dtype (exact and fast), and the prefill
-    grid M in {128, 512, 2048} x both FFN shapes. Random-code blocks (synth.random_blocks): timing only."""
+    """Cold-ring GEMV time for every Llama-3-8B linear shape and dtype (exact and fast), OpenQuant and the
+    quantized embedding lookup, and the prefill grid M in {128, 512, 2048} x both FFN shapes. Random-code blocks
+    (synth.random_blocks): timing only."""
     from tcb_amd import MODE_EXACT, MODE_FAST, Q4, Q4K, Q6K, Q8, _lib, synth
     L = _lib.lib()
     ctx = tb.ctx
@@ -187,6 +188,38 @@ def shape_table(tb):
             w.release()
         xb.free()
         cb.free()
+    # OpenQuant (dequantize a whole store to fp32) and the quantized embedding lookup: HBM-bound, bytes = blocks read
+    # + fp32 written
+    other = {}
+    for dt, n, k in ((Q4K, 14336, 4096), (Q6K, 14336, 4096), (Q8, 4096, 4096)):
+        w = tb.FromQuantized(dt, synth.random_blocks(dt, n, k, seed=9), n, k)
+        ob = ctx.alloc(n * k * 4)
+        tb.OpenQuant(ob, w)
+        ctx.sync()
+        g = capture(tb, lambda: tb.OpenQuant(ob, w))
+        time_graph(tb, g, 2)
+        us = time_graph(tb, g, 5) * 1e3 / 5
+        L.trhip_graph_destroy(g)
+        moved = w.device_bytes() + n * k * 4
+        other["open_q %s %dx%d" % (names[dt], n, k)] = {"us": round(us, 1), "GB/s": round(moved / us / 1e3, 1)}
+        ob.free()
+        w.release()
+    emb = tb.FromQuantized(Q6K, synth.random_blocks(Q6K, 128256, 4096, seed=11), 128256, 4096)
+    for ntok in (1, 16, 512):
+        ob = ctx.alloc(ntok * 4096 * 4)
+        idx = np.random.default_rng(ntok).integers(0, 128256, ntok)
+        tb.Embedding(ob, emb, idx)
+        ctx.sync()
+        e0, e1 = ctx.event(), ctx.event()
+        ctx.record(e0)
+        for _ in range(20):
+            tb.Embedding(ob, emb, idx)
+        ctx.record(e1)
+        ctx.sync()
+        us = ctx.elapsed_ms(e0, e1) * 1e3 / 20
+        other["embedding q6_k 128256x4096, %d tokens" % ntok] = {"us": round(us, 2)}
+        ob.free()
+    emb.release()
     prefill = {}
     for n, k in ((14336, 4096), (4096, 14336)):
         w = tb.FromQuantized(Q4K, synth.random_blocks(Q4K, n, k, seed=7), n, k)
@@ -205,7 +238,7 @@ def shape_table(tb):
             Xb.free()
             Cb.free()
         w.release()
-    return {"gemv_cold_ring": gemv, "prefill": prefill}
+    return {"gemv_cold_ring": gemv, "prefill": prefill, "open_q_and_embedding": other}
 
 
 def profile_kernel(a):
@@ -335,6 +368,21 @@ def main():
         return out, ms_cold * 1e3 / steps, ms_warm * 1e3 / steps
 
     gpu_out, us_cold, us_warm = measure(mode)
+
+    # single-launch streaming-read ceiling: the same number of bytes read once by trhip_read_probe, over a cold ring
+    # of plain buffers timed the same way; no kernel that streams these bytes in one launch can be faster
+    rbytes = wbytes // 16 * 16
+    rring = [ctx.alloc(rbytes) for _ in range(ring_n)]
+    for b in rring:
+        b.fill(1)
+    ctx.read_probe(rring[0], rbytes)
+    ctx.sync()
+    g_read = capture(tb, lambda: [ctx.read_probe(b, rbytes) for b in rring])
+    time_graph(tb, g_read, warm_replays)
+    us_read = time_graph(tb, g_read, replays) * 1e3 / steps
+    L.trhip_graph_destroy(g_read)
+    for b in rring:
+        b.free()
     gbs_cold = abytes / (us_cold * 1e-6) / 1e9
     gbs_warm = abytes / (us_warm * 1e-6) / 1e9
     other = MODE_EXACT if mode == MODE_FAST else MODE_FAST
@@ -413,6 +461,11 @@ def main():
         "us_per_gemv": round(us_cold, 3),
         "hbm_frac_of_peak": round(gbs_cold / HBM_PEAK_GBS, 4),
         "warm": {"us_per_gemv": round(us_warm, 3), "GB/s": round(gbs_warm, 1)},
+        "read_ceiling": {"us_per_launch": round(us_read, 3), "GB/s": round(rbytes / (us_read * 1e-6) / 1e9, 1),
+                         "frac_of_peak": round(rbytes / (us_read * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                         "gemv_frac_of_ceiling": round(us_read / us_cold, 4),
+                         "workload": "trhip_read_probe: %d bytes read once per launch, cold ring of %d buffers" % (
+                             rbytes, ring_n)},
         other_name + "_mode": {"us_per_gemv": round(us_other, 3), "GB/s": round(abytes / (us_other * 1e-6) / 1e9, 1),
                                "warm_us_per_gemv": round(us_other_warm, 3)},
         "roofline": {"bound": "hbm", "achieved": round(gbs_cold, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -159,6 +159,11 @@ int trhip_gemm_q_swiglu(trhip_ctx *ctx, const trhip_wstore *w, const float *x, f
 int trhip_quantize_q8(trhip_ctx *ctx, const float *x, int64_t M, int64_t K, int blk, int8_t *q, float *d,
                       int16_t *bs);
 
+/* Diagnostic with no counterpart in the reference: reads `bytes` of device memory at p once (p and
+ * bytes 16-byte aligned) and writes nothing. One launch over a buffer that is not in the caches times
+ * the device's single-launch streaming-read ceiling, the floor the GEMV kernels are measured against. */
+int trhip_read_probe(trhip_ctx *ctx, const void *p, int64_t bytes);
+
 #ifdef __cplusplus
 }
 #endif

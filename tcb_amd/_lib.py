@@ -46,6 +46,7 @@ SIGNATURES = [
     ("trhip_gemm_q", INT, [P, P, I64, I64, P, P, I64, I64, INT, INT]),
     ("trhip_gemm_q_actq", INT, [P, P, I64, I64, P, P, I64, I64, INT]),
     ("trhip_open_q", INT, [P, P, I64, I64, P]),
+    ("trhip_read_probe", INT, [P, P, I64]),
     ("trhip_embedding_q", INT, [P, P, P, I64, P]),
     ("trhip_quantize_q8", INT, [P, P, I64, I64, INT, P, P, P]),
     ("trhip_swiglu", INT, [P, P, I64, I64, P]),

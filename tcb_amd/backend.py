@@ -120,6 +120,10 @@ class Context:
     def record(self, ev):
         _check(_lib.lib().trhip_event_record(self.h, ev), self.h)
 
+    def read_probe(self, buf, nbytes=None):
+        """Read nbytes of buf once on the device (the single-launch streaming-read ceiling; writes nothing)."""
+        _check(_lib.lib().trhip_read_probe(self.h, buf.addr(), buf.nbytes if nbytes is None else nbytes), self.h)
+
     @staticmethod
     def elapsed_ms(a, b):
         ms = ctypes.c_float()

@@ -585,6 +585,15 @@ int trhip_open_q(trhip_ctx *ctx, const trhip_wstore *w, int64_t elem_off, int64_
     return launch_dequant(ctx, w, elem_off / be, n / be, out);
 }
 
+int trhip_read_probe(trhip_ctx *ctx, const void *p, int64_t bytes) {
+    if (!ctx || bytes < 0) return TRHIP_ERR_INVALID;
+    if (bytes == 0) return TRHIP_OK;
+    if (!p || bytes % 16 || reinterpret_cast<uintptr_t>(p) % 16)
+        return fail(ctx, TRHIP_ERR_INVALID, "read_probe: p and bytes must be 16-byte aligned");
+    DevGuard g(ctx);
+    return launch_read_probe(ctx, p, bytes);
+}
+
 int trhip_embedding_q(trhip_ctx *ctx, const trhip_wstore *w, const int64_t *idx, int64_t nidx, float *out) {
     if (!ctx || !w || nidx < 0) return TRHIP_ERR_INVALID;
     if (nidx == 0) return TRHIP_OK;

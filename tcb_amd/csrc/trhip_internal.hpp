@@ -187,6 +187,7 @@ int launch_gemm_rows_fast(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, i
                           int64_t M, bool acc);
 int launch_quantize_q8(trhip_ctx *ctx, const float *x, int64_t M, int64_t K, int blk, int8_t *q, float *d,
                        int16_t *bs, uint8_t *bad, uint16_t *sj);
+int launch_read_probe(trhip_ctx *ctx, const void *p, int64_t bytes);
 int launch_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                 int64_t M, bool acc, const int8_t *q, const float *d, const int16_t *bs, const uint8_t *bad,
                 const uint16_t *sj);
