@@ -51,86 +51,81 @@ __global__ void repack_kernel(const uint8_t *__restrict__ raw, uint8_t *__restri
     }
 }
 
-// Dequantize 32 consecutive elements (one 32-element group) per thread; tensor/quant.go:139-205.
+// Elements 4f .. 4f+3 of block bi, dequantized as tensor/quant.go:139-205 (one thread per four outputs, so a
+// wave's stores cover 1 KB of contiguous output). Every code word is one aligned dword of its plane: the four
+// elements share their scale and min, and their bytes are contiguous in the repacked planes.
 template <int DT>
-__device__ void dequant_group(const Planes p, int64_t bi, int G, float *y) {
+__device__ __forceinline__ float4 dequant4(const Planes p, int64_t bi, int f) {
+    const int e = 4 * f;
+    float y[4];
     if (DT == kQ8) {
-        float d = f16_to_f32(p.d[bi]);
-        const int8_t *c = reinterpret_cast<const int8_t *>(p.qs + bi * 32);
-        for (int j = 0; j < 32; j++) y[j] = (float)c[j] * d;
-    } else if (DT == kQ4) {
-        float d = f16_to_f32(p.d[bi]);
-        const uint8_t *c = p.qs + bi * 16;
-        // group G of a q4 block is the whole block (32 elements)
-        for (int j = 0; j < 16; j++) {
-            y[j] = (float)((int)(c[j] & 0xF) - 8) * d;
-            y[j + 16] = (float)((int)(c[j] >> 4) - 8) * d;
+        const float d = f16_to_f32(p.d[bi]);
+        const uint32_t c = *reinterpret_cast<const uint32_t *>(p.qs + bi * 32 + e);
+#pragma unroll
+        for (int k = 0; k < 4; k++) y[k] = (float)(int8_t)((c >> (8 * k)) & 0xFF) * d;
+    } else if (DT == kQ4) {  // element j < 16: low nibble of byte j; j >= 16: high nibble of byte j - 16
+        const float d = f16_to_f32(p.d[bi]);
+        const uint32_t c = *reinterpret_cast<const uint32_t *>(p.qs + bi * 16 + (e & 15));
+        const int sh = e < 16 ? 0 : 4;
+#pragma unroll
+        for (int k = 0; k < 4; k++) y[k] = (float)((int)((c >> (8 * k + sh)) & 0xF) - 8) * d;
+    } else if (DT == kQ4K) {  // sub-block j = e / 32: low nibbles of group j / 2 for even j, high for odd j
+        const uint4 h = *reinterpret_cast<const uint4 *>(p.aux + bi * 16);  // d, dmin, scales[12]
+        const float d = f16_to_f32((uint16_t)(h.x & 0xFFFF)), dmin = f16_to_f32((uint16_t)(h.x >> 16));
+        const int j = e >> 5, g = e >> 6, ee = e & 31;
+        uint32_t sc_lo, sc_hi, m_lo, m_hi;
+        q4k_scales(h.y, h.z, h.w, sc_lo, sc_hi, m_lo, m_hi);
+        const float scv = ubyte_f(j < 4 ? sc_lo : sc_hi, j & 3), mv = ubyte_f(j < 4 ? m_lo : m_hi, j & 3);
+        const float d1 = d * scv, m1 = dmin * mv;
+        const uint32_t c = *reinterpret_cast<const uint32_t *>(p.qs + bi * 128 + q4k_pos(32 * g + ee));
+        const int sh = (j & 1) ? 4 : 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) y[k] = d1 * (float)((c >> (8 * k + sh)) & 0xF) - m1;
+    } else {  // q6_k, 32-element group k4 of half n: elements 128n + 32k4 + ee
+        const float d = f16_to_f32(p.d[bi]);
+        const int n = e >> 7, k4 = (e >> 5) & 3, ee = e & 31, t = ee >> 3, l = ee & 7;
+        const uint32_t lo = *reinterpret_cast<const uint32_t *>(p.qs + bi * 128 + 32 * t + 16 * n + 8 * (k4 & 1) + l);
+        const uint32_t hb = *reinterpret_cast<const uint32_t *>(p.aux + bi * 64 + 16 * t + 8 * n + l);
+        const float sc = (float)(int8_t)p.sc[bi * 16 + 8 * n + 2 * k4 + ee / 16];
+        const int sh = k4 < 2 ? 0 : 4;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int code = (int)((lo >> (8 * k + sh)) & 0xF) | (int)(((hb >> (8 * k + 2 * k4)) & 3) << 4);
+            y[k] = d * sc * (float)(code - 32);
         }
-    } else if (DT == kQ4K) {
-        const uint8_t *h = p.aux + bi * 16;
-        float d = f16_to_f32((uint16_t)(h[0] | (h[1] << 8)));
-        float dmin = f16_to_f32((uint16_t)(h[2] | (h[3] << 8)));
-        const uint8_t *s = h + 4;
-        int j = G;  // sub-block j: low nibbles of group j/2 for even j, high nibbles for odd j
-        uint8_t scv, mv;
-        if (j < 4) {
-            scv = s[j] & 63;
-            mv = s[j + 4] & 63;
-        } else {
-            scv = (uint8_t)((s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4));
-            mv = (uint8_t)((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
-        }
-        float d1 = d * (float)scv, m1 = dmin * (float)mv;
-        const uint8_t *q = p.qs + bi * 128;
-        int g = j >> 1;
-        for (int e = 0; e < 32; e++) {
-            uint8_t b = q[q4k_pos(32 * g + e)];  // old byte 32g + e
-            uint32_t code = (j & 1) ? (b >> 4) : (b & 0xF);
-            y[e] = d1 * (float)code - m1;
-        }
-    } else {  // q6_k, 32-element group G = 4n + k: elements 128n + 32k + e
-        float d = f16_to_f32(p.d[bi]);
-        const int8_t *sc = reinterpret_cast<const int8_t *>(p.sc + bi * 16);
-        const uint8_t *ql = p.qs + bi * 128, *qh = p.aux + bi * 64;
-        int n = G >> 2, k = G & 3;
-        for (int e = 0; e < 32; e++) {
-            int t = e >> 3, l = e & 7;
-            uint8_t lo = ql[32 * t + 16 * n + 8 * (k & 1) + l];
-            uint8_t hb = qh[16 * t + 8 * n + l];
-            int nib = (k < 2) ? (lo & 0xF) : (lo >> 4);
-            int code = nib | (((hb >> (2 * k)) & 3) << 4);
-            int is = e / 16;
-            y[e] = d * (float)sc[8 * n + is + 2 * k] * (float)(code - 32);
-        }
+    }
+    return make_float4(y[0], y[1], y[2], y[3]);
+}
+
+// out may be any float pointer: aligned outputs take one 16-byte store, others four 4-byte stores
+__device__ __forceinline__ void store4(float *out, int64_t i, float4 v, bool aligned) {
+    if (aligned) {
+        reinterpret_cast<float4 *>(out)[i] = v;
+    } else {
+        out[4 * i] = v.x;
+        out[4 * i + 1] = v.y;
+        out[4 * i + 2] = v.z;
+        out[4 * i + 3] = v.w;
     }
 }
 
 template <int DT>
-__global__ void dequant_kernel(const Planes p, int64_t block0, int64_t ngroups, float *__restrict__ out) {
-    int64_t gi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gi >= ngroups) return;
-    constexpr int per = block_elems(DT) / 32;
-    int64_t bi = block0 + gi / per;
-    int G = (int)(gi % per);
-    float y[32];
-    dequant_group<DT>(p, bi, G, y);
-    float4 *o = reinterpret_cast<float4 *>(out + gi * 32);
-    for (int i = 0; i < 8; i++) o[i] = make_float4(y[4 * i], y[4 * i + 1], y[4 * i + 2], y[4 * i + 3]);
+__global__ void dequant_kernel(const Planes p, int64_t block0, int64_t n4, float *__restrict__ out, bool aligned) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n4) return;
+    constexpr int per = block_elems(DT) / 4;
+    store4(out, i, dequant4<DT>(p, block0 + i / per, (int)(i % per)), aligned);
 }
 
 template <int DT>
-__global__ void embedding_kernel(const Planes p, int64_t N, const int64_t *__restrict__ idx, int64_t nidx,
-                                 float *__restrict__ out) {
-    constexpr int per = block_elems(DT) / 32;
-    int64_t groups_per_row = p.nb * per;
-    int64_t gi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gi >= nidx * groups_per_row) return;
-    int64_t i = gi / groups_per_row, gr = gi % groups_per_row;
-    int64_t r = idx[i];
-    float y[32];
-    dequant_group<DT>(p, r * p.nb + gr / per, (int)(gr % per), y);
-    float4 *o = reinterpret_cast<float4 *>(out + gi * 32);
-    for (int k = 0; k < 8; k++) o[k] = make_float4(y[4 * k], y[4 * k + 1], y[4 * k + 2], y[4 * k + 3]);
+__global__ void embedding_kernel(const Planes p, const int64_t *__restrict__ idx, int64_t nidx,
+                                 float *__restrict__ out, bool aligned) {
+    constexpr int per = block_elems(DT) / 4;
+    const int64_t row4 = p.nb * per;  // float4 per output row
+    const int64_t gi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gi >= nidx * row4) return;
+    const int64_t i = gi / row4, f = gi % row4;
+    store4(out, gi, dequant4<DT>(p, idx[i] * p.nb + f / per, (int)(f % per)), aligned);
 }
 
 template <template <int> class F, typename... A>
@@ -161,11 +156,12 @@ struct RepackRun {
 template <int DT>
 struct DequantRun {
     static int run(trhip_ctx *ctx, const trhip_wstore *w, int64_t block0, int64_t nblocks, float *out) {
-        int64_t ngroups = nblocks * (block_elems(DT) / 32);
-        if (ngroups == 0) return TRHIP_OK;
+        const int64_t n4 = nblocks * (block_elems(DT) / 4);
+        if (n4 == 0) return TRHIP_OK;
         const int threads = 256;
-        hipLaunchKernelGGL(dequant_kernel<DT>, dim3((unsigned)((ngroups + threads - 1) / threads)), dim3(threads), 0,
-                           ctx->stream, w->planes(), block0, ngroups, out);
+        if ((n4 + threads - 1) / threads >= ((int64_t)1 << 31)) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "open_q: too many elements");
+        hipLaunchKernelGGL(dequant_kernel<DT>, dim3((unsigned)((n4 + threads - 1) / threads)), dim3(threads), 0,
+                           ctx->stream, w->planes(), block0, n4, out, reinterpret_cast<uintptr_t>(out) % 16 == 0);
         return launch_check(ctx, "open_q");
     }
 };
@@ -173,11 +169,13 @@ struct DequantRun {
 template <int DT>
 struct EmbedRun {
     static int run(trhip_ctx *ctx, const trhip_wstore *w, const int64_t *idx, int64_t nidx, float *out) {
-        int64_t total = nidx * w->nb * (block_elems(DT) / 32);
+        const int64_t total = nidx * w->nb * (block_elems(DT) / 4);
         if (total == 0) return TRHIP_OK;
         const int threads = 256;
+        if ((total + threads - 1) / threads >= ((int64_t)1 << 31))
+            return fail(ctx, TRHIP_ERR_UNSUPPORTED, "embedding_q: too many elements");
         hipLaunchKernelGGL(embedding_kernel<DT>, dim3((unsigned)((total + threads - 1) / threads)), dim3(threads), 0,
-                           ctx->stream, w->planes(), w->N, idx, nidx, out);
+                           ctx->stream, w->planes(), idx, nidx, out, reinterpret_cast<uintptr_t>(out) % 16 == 0);
         return launch_check(ctx, "embedding_q");
     }
 };

@@ -63,7 +63,11 @@ def test_open_quant_golden(backend, dt, seed, want, at, sample):
     out2 = backend.ctx.alloc(3 * elems * 4)
     backend.OpenQuant(out2, w, offset=7 * elems, n=3 * elems)
     same_bits(out2.download(np.float32, 3 * elems), y[7 * elems:10 * elems])
-    for b in (out, out2):
+    # an output that is not 16-byte aligned (one float into the buffer)
+    out3 = backend.ctx.alloc(3 * elems * 4 + 4)
+    backend.OpenQuant((out3, 4), w, offset=7 * elems, n=3 * elems)
+    same_bits(out3.download(np.float32, 3 * elems, byte_offset=4), y[7 * elems:10 * elems])
+    for b in (out, out2, out3):
         b.free()
     w.release()
 
@@ -383,9 +387,13 @@ def test_embedding(backend, dt):
     out = backend.ctx.alloc(len(idx) * D * 4)
     backend.Embedding(out, w, idx)
     same_bits(out.download(np.float32, len(idx) * D), O.embedding(dt, raw, D, idx))
+    out1 = backend.ctx.alloc(len(idx) * D * 4 + 4)  # an output that is not 16-byte aligned
+    backend.Embedding((out1, 4), w, idx)
+    same_bits(out1.download(np.float32, len(idx) * D, byte_offset=4), O.embedding(dt, raw, D, idx))
     with pytest.raises(TrhipError):
         backend.Embedding(out, w, [5])
-    out.free()
+    for b in (out, out1):
+        b.free()
     w.release()
 
 
