@@ -159,8 +159,8 @@ def decode_sweep(tb, batches, mode, replays=5):
 
 
 def shape_table(tb):
-    """Cold-ring GEMV time for every Llama-3-8B linear shape and dtype (exact and fast), OpenQuant and the
-    quantized embedding lookup, and the prefill grid M in {128, 512, 2048} x both FFN shapes. Random-code blocks
+    """Cold-ring GEMV time for every Llama-3-8B linear shape and dtype (exact and fast), the M > 1 path at the
+    configs' batch sizes, OpenQuant and the quantized embedding lookup, and the prefill grid M in {128, 512, 2048} x both FFN shapes. Random-code blocks
     (synth.random_blocks): timing only."""
     from tcb_amd import MODE_EXACT, MODE_FAST, Q4, Q4K, Q6K, Q8, _lib, synth
     L = _lib.lib()
@@ -188,6 +188,27 @@ def shape_table(tb):
             w.release()
         xb.free()
         cb.free()
+    # the M > 1 fp32 path (batched decode): q4_0 FFN shapes at batch 8, q4_k at batch 16, the q6_k output head at
+    # batch 16; one weight copy, timed as graph replays (the weights exceed the MALL except for the 4096-row shapes)
+    rows = {}
+    for dt, n, k, m in ((Q4, 14336, 4096, 8), (Q4, 4096, 14336, 8), (Q4K, 14336, 4096, 16), (Q4K, 4096, 14336, 16),
+                        (Q6K, 128256, 4096, 16)):
+        w = tb.FromQuantized(dt, synth.random_blocks(dt, n, k, seed=12), n, k)
+        Xb = ctx.to_device(synth.activations(m, k, seed=13))
+        Cb = ctx.alloc(m * n * 4)
+        res = {}
+        for md in (MODE_EXACT, MODE_FAST):
+            tb.GemmSet(m, n, k, Xb, w, Cb, mode=md)
+            ctx.sync()
+            g = capture(tb, lambda: tb.GemmSet(m, n, k, Xb, w, Cb, mode=md))
+            time_graph(tb, g, 2)
+            us = time_graph(tb, g, 10) * 1e3 / 10
+            L.trhip_graph_destroy(g)
+            res["fast" if md else "exact"] = {"us": round(us, 1), "GB/s": round(w.device_bytes() / us / 1e3, 1)}
+        rows["%s %dx%d M=%d" % (names[dt], n, k, m)] = res
+        Xb.free()
+        Cb.free()
+        w.release()
     # OpenQuant (dequantize a whole store to fp32) and the quantized embedding lookup: HBM-bound, bytes = blocks read
     # + fp32 written
     other = {}
@@ -238,7 +259,7 @@ def shape_table(tb):
             Xb.free()
             Cb.free()
         w.release()
-    return {"gemv_cold_ring": gemv, "prefill": prefill, "open_q_and_embedding": other}
+    return {"gemv_cold_ring": gemv, "rows": rows, "prefill": prefill, "open_q_and_embedding": other}
 
 
 def profile_kernel(a):
