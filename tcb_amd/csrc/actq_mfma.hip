@@ -779,6 +779,251 @@ __global__ void fm_sum_kernel(const float *__restrict__ partial, float *__restri
     }
 }
 
+
+// Fast M > 1 for q6_k (tolerance), on v_mfma_f32_16x16x32_f16. halves_kernel writes each activation row in
+// 256-element chunks as x' = x * 2^-E (E from the chunk's largest |x|, so |x'| < 1) split into two f16 planes,
+// hi = f16(x') * 2^11 (exact scaling) and lo = f16((x' - f16(x')) * 2^11): hi + lo holds x' * 2^11 to about 2^-23 of
+// the chunk's largest element, and both terms stay in the normal f16 range. The codes q - 32 are exact small integers
+// in f16 (built from their bytes as 0x6400 | byte = 1024 + byte, then one packed f16 subtraction), and
+// sc = (sc & ~1) + (sc & 1) makes both weight planes (q - 32) (sc & ~1) (even, at most 4096 in magnitude) and
+// (q - 32) (sc & 1) exact in f16, so every MFMA product is exact and one fp32 accumulator takes the whole block:
+//   acc += d * D * 2^(E-11),  D = sum over the block of (hi + lo) (q - 32) sc
+// Lane l holds 8 halves of row / column l % 16 at k-slice l / 16; result register v of lane l is row 4 (l / 16) + v,
+// column l % 16. Rows of x holding NaN / Inf take exact float dot products, as in the q4_k kernels.
+// Workgroup (tile, slice): 16 activation rows x 128 weight rows over blocks [bps s, bps s + bps); wave w owns weight
+// rows 32 w .. +31 as two 16-column tiles. A block's two planes are staged in LDS (double-buffered) as 16-byte slots
+// 64 s + l (step s, lane l), so every MFMA operand read is one conflict-free ds_read_b128.
+// (The same scheme for q8_0 / q4_0, with a per-block scale FMA after each step, measured slower than the exact
+// kernel at M = 2..16: 37-40 us against 25-38 us at 14336 x 4096; those dtypes run exact.)
+constexpr int FH_PLANE = 8 * 1024;                   // one f16 plane of a 16-row chunk
+constexpr int FH_STAGE = 2 * FH_PLANE + F16_TM * 4;  // hi, lo, exponents
+constexpr size_t FH_LDS = 2 * FH_STAGE + (F16_TM + 1) * sizeof(int);
+
+// One wave per (row m, chunk b): exponent, the two f16 planes and the NaN/Inf flag.
+__global__ __launch_bounds__(256) void halves_kernel(const float *__restrict__ x, int64_t M, int64_t K,
+                                                     uint16_t *__restrict__ hi, uint16_t *__restrict__ lo,
+                                                     int *__restrict__ ex, uint8_t *__restrict__ bad) {
+    const int lane = threadIdx.x & 63;
+    const int64_t nb = K / 256;
+    const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (gw >= M * nb) return;  // wave-uniform
+    const int64_t m = gw / nb, b = gw % nb;
+    const float4 v = reinterpret_cast<const float4 *>(x + m * K + 256 * b)[lane];
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    const bool fin = (fabsf(v.x) <= FLT_MAX) && (fabsf(v.y) <= FLT_MAX) && (fabsf(v.z) <= FLT_MAX) &&
+                     (fabsf(v.w) <= FLT_MAX);
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    const bool allfin = __all(fin);
+    int E = 0;
+    if (allfin && amax > 0.0f) frexpf(amax, &E);  // amax = f 2^E, f in [0.5, 1)
+    const float xv[4] = {v.x, v.y, v.z, v.w};
+    uint16_t h[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float xs = allfin ? ldexpf(xv[i], -E) : 0.0f;  // |xs| < 1
+        const _Float16 xh = (_Float16)xs;
+        h[i] = __builtin_bit_cast(uint16_t, (_Float16)((float)xh * 2048.0f));
+        l[i] = __builtin_bit_cast(uint16_t, (_Float16)((xs - (float)xh) * 2048.0f));
+    }
+    const int64_t o = (m * K + 256 * b) / 4 + lane;  // 4 halves per lane
+    reinterpret_cast<uint2 *>(hi)[o] = make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
+    reinterpret_cast<uint2 *>(lo)[o] = make_uint2(l[0] | ((uint32_t)l[1] << 16), l[2] | ((uint32_t)l[3] << 16));
+    if (lane == 0) {
+        ex[m * nb + b] = E - 11;
+        bad[m * nb + b] = allfin ? 0 : 1;
+    }
+}
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+// (native vector types: HIP's uint2 / uint4 structs are copied through scratch memory when carried across loops)
+struct Q6Regs {  // one 16-column tile's weight registers for one q6_k block
+    u32x4 ql0, ql1, qh, sc;  // the lane's 32 ql bytes and 16 qh bytes (repacked k-slice ks), the 16 scales
+    uint32_t d;
+};
+
+__device__ __forceinline__ void q6_load(Q6Regs &r, const Planes p, int64_t row, int64_t c, int ks) {
+    const int64_t bi = row * p.nb + c;
+    const u32x4 *ql = reinterpret_cast<const u32x4 *>(p.qs + bi * 128 + 32 * ks);
+    r.ql0 = ql[0];
+    r.ql1 = ql[1];
+    r.qh = *reinterpret_cast<const u32x4 *>(p.aux + bi * 64 + 16 * ks);
+    r.sc = *reinterpret_cast<const u32x4 *>(p.sc + bi * 16);
+    r.d = p.d[bi];
+}
+
+// Bytes 0, 1 (hi = false) or 2, 3 of w as the f16 pair (1024 + byte0, 1024 + byte1): v_perm_b32 places each byte
+// under 0x64, the f16 exponent of 1024.
+__device__ __forceinline__ h2 f16_pair(uint32_t w, bool hi) {
+    return __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, w, hi ? 0x04030402u : 0x04010400u));
+}
+
+// The 8 codes of step s (32-element group k4 = s % 4 of half n = s / 4) at k-slice ks as exact f16 q - 32: ql words
+// 4n + 2 (k4 & 1), qh words 2n.
+__device__ __forceinline__ v8h q6_codes(const Q6Regs &r, int s) {
+    const int n = s >> 2, k4 = s & 3;
+    const uint32_t qw[8] = {r.ql0.x, r.ql0.y, r.ql0.z, r.ql0.w, r.ql1.x, r.ql1.y, r.ql1.z, r.ql1.w};
+    const uint32_t hw[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+    const int sh = k4 >= 2 ? 4 : 0;
+    const uint32_t w0 = ((qw[4 * n + 2 * (k4 & 1)] >> sh) & 0x0F0F0F0Fu) | (((hw[2 * n] >> (2 * k4)) & 0x03030303u) << 4);
+    const uint32_t w1 =
+        ((qw[4 * n + 2 * (k4 & 1) + 1] >> sh) & 0x0F0F0F0Fu) | (((hw[2 * n + 1] >> (2 * k4)) & 0x03030303u) << 4);
+    const h2 off = (h2){(_Float16)1056.0f, (_Float16)1056.0f};
+    const h2 a = f16_pair(w0, false) - off, b = f16_pair(w0, true) - off;
+    const h2 c = f16_pair(w1, false) - off, d = f16_pair(w1, true) - off;
+    return (v8h){a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+}
+
+template <bool ACC>
+__global__ __launch_bounds__(FM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void fastm16_q6k(
+    const Planes p, int64_t N, int64_t row0, int64_t M, int64_t K, const float *__restrict__ x,
+    const uint16_t *__restrict__ xh, const uint16_t *__restrict__ xl, const int *__restrict__ ex,
+    const uint8_t *__restrict__ bad, int64_t bps, float *__restrict__ c, float *__restrict__ partial) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    int *rowbad = reinterpret_cast<int *>(lds + 2 * FH_STAGE);
+    int *anybad = rowbad + F16_TM;
+    const int nc = (int)(K / 256);  // blocks per row
+    const int tid = threadIdx.x, lane = tid & 63, ks = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int64_t tmi, tni;
+    tile_of(blockIdx.x, (M + F16_TM - 1) / F16_TM, (N + FM_TN - 1) / FM_TN, tmi, tni);
+    const int64_t n0 = tni * FM_TN, m0 = tmi * F16_TM;
+    const int c0 = (int)(blockIdx.y * bps), c1 = (int)((blockIdx.y + 1) * bps < nc ? (blockIdx.y + 1) * bps : nc);
+    tile_row_flags<F16_TM, FM_THREADS>(bad, m0, M, nc, rowbad, anybad);
+
+    // staging: 16-byte pieces P = tid and tid + 256 of each plane: row P / 32, piece j = P % 32 (halves 8j .. +7)
+    // = step j / 4, k-slice j % 4, i.e. slot 64 (j / 4) + 16 (j % 4) + row; threads < 16 one exponent
+    const uint16_t *hsrc[2];
+    int hslot[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int P = tid + 256 * i, r = P >> 5, j = P & 31;
+        hsrc[i] = xh + (m0 + r < M ? m0 + r : M - 1) * K + 8 * j;
+        hslot[i] = 64 * (j >> 2) + 16 * (j & 3) + r;
+    }
+    const int64_t lo_off = xl - xh;  // the lo plane sits at the same offsets from xl
+    const int64_t egm = m0 + (tid & 15) < M ? m0 + (tid & 15) : M - 1;
+    v4i sa[4];
+    int se = 0;
+    auto fetch_a = [&](int b) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            sa[i] = *reinterpret_cast<const v4i *>(hsrc[i] + 256 * (int64_t)b);
+            sa[2 + i] = *reinterpret_cast<const v4i *>(hsrc[i] + lo_off + 256 * (int64_t)b);
+        }
+        if (tid < F16_TM) se = ex[egm * nc + b];
+    };
+    auto put_a = [&](int buf) {
+        uint8_t *st = lds + buf * FH_STAGE;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            reinterpret_cast<v4i *>(st)[hslot[i]] = sa[i];
+            reinterpret_cast<v4i *>(st + FH_PLANE)[hslot[i]] = sa[2 + i];
+        }
+        if (tid < F16_TM) reinterpret_cast<int *>(st + 2 * FH_PLANE)[tid] = se;
+    };
+
+    int64_t wrow[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        const int nl = 32 * w + 16 * t + (lane & 15);
+        wrow[t] = row0 + ((n0 + nl) < N ? (n0 + nl) : N - 1);
+    }
+    // two weight register sets used alternately (blocks b and b + 1), so a block's weights are requested during
+    // the previous block without any copy of registers whose loads are still in flight (such a copy waits for every
+    // outstanding load, the next block's staging included)
+    Q6Regs wA[2], wB[2];
+    auto fetch_w = [&](Q6Regs(&wr)[2], int b) {
+#pragma unroll
+        for (int t = 0; t < 2; t++) q6_load(wr[t], p, wrow[t], b, ks);
+    };
+
+    float accf[2][4];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) accf[t][v] = 0.0f;
+    // every slice holds at least one chunk; the prefetches below are issued unconditionally (the last chunk's
+    // re-read, when there is no next one), so the wait counts stay static and never fall back to waiting for
+    // everything outstanding
+    auto last = [&](int b) { return b < c1 ? b : c1 - 1; };
+    fetch_a(c0);
+    fetch_w(wA, c0);
+    put_a(0);
+    fetch_a(last(c0 + 1));
+    __syncthreads();
+
+    const v4f zero = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+    auto chunk = [&](int b, const Q6Regs(&cw)[2]) {
+        const uint8_t *st = lds + ((b - c0) & 1) * FH_STAGE;
+        const v8h *ph = reinterpret_cast<const v8h *>(st), *pq = reinterpret_cast<const v8h *>(st + FH_PLANE);
+        v4f acc[2] = {zero, zero};
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            const v8h ah = ph[64 * s + lane], al = pq[64 * s + lane];
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const v8h q = q6_codes(cw[t], s);
+                // scale of this lane's 16-element group (2 s + ks / 2), as even part and low bit
+                const uint32_t scw = s < 2 ? cw[t].sc.x : s < 4 ? cw[t].sc.y : s < 6 ? cw[t].sc.z : cw[t].sc.w;
+                const int sc = (int)(int8_t)((scw >> (16 * (s & 1) + 8 * (ks >> 1))) & 0xFF);
+                const _Float16 se2 = (_Float16)(float)(sc & ~1), so = (_Float16)(float)(sc & 1);
+                const v8h q1 = q * se2, q2 = q * so;
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, q1, acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, q1, acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, q2, acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, q2, acc[t], 0, 0, 0);
+            }
+        }
+        if (b + 1 < c1) put_a((b + 1 - c0) & 1);
+        fetch_a(last(b + 2));
+        const int *exs = reinterpret_cast<const int *>(st + 2 * FH_PLANE);
+        const int4 e4 = *reinterpret_cast<const int4 *>(exs + 4 * ks);
+        const int ev[4] = {e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const float dk = f16_to_f32((uint16_t)cw[t].d);
+#pragma unroll
+            for (int v = 0; v < 4; v++) accf[t][v] = accf[t][v] + ldexpf(dk * acc[t][v], ev[v]);
+        }
+        __syncthreads();
+    };
+    for (int b = c0; b < c1; b += 2) {
+        fetch_w(wB, last(b + 1));
+        chunk(b, wA);
+        if (b + 1 >= c1) break;
+        fetch_w(wA, last(b + 2));
+        chunk(b + 1, wB);
+    }
+
+    float *dst = partial ? partial + (int64_t)blockIdx.y * M * N : c;
+    const bool acc_c = ACC && partial == nullptr;
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        const int64_t gn = n0 + 32 * w + 16 * t + (lane & 15);
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int mloc = 4 * ks + v;
+            if (gn < N && rowbad[mloc] == 0) {
+                float *o = dst + (m0 + mloc) * N + gn;
+                *o = acc_c ? *o + accf[t][v] : accf[t][v];
+            }
+        }
+    }
+    if (!*anybad) return;
+    for (int i = tid; i < F16_TM * FM_TN; i += FM_THREADS) {  // rows holding NaN/Inf: exact float dot products
+        const int ml = i / FM_TN, nl = i % FM_TN;
+        const int64_t gn2 = n0 + nl;
+        if (rowbad[ml] != 1 || gn2 >= N) continue;
+        const int64_t gm = m0 + ml;
+        const float v = blockIdx.y == 0 ? exact_dot_row<kQ6K>(p, row0 + gn2, x + gm * K, K) : 0.0f;
+        float *o = dst + gm * N + gn2;
+        *o = acc_c ? *o + v : v;
+    }
+}
+
 }  // namespace
 
 int launch_actq_mfma(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
@@ -801,20 +1046,25 @@ int launch_actq_mfma(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_
 
 namespace trhip {
 
-// Fast-mode M > 1 for q4_k (tolerance 1e-4): digit planes of x, then the int8 MFMA kernel over K slices.
+// Fast-mode M > 1 for q4_k and q6_k (tolerance): x as fixed-point planes (q4_k: int8 digits for fastm_mfma_q4k /
+// fastm16_mfma_q4k; q6_k: two f16 planes for fastm16_q6k on 16-row tiles), the MFMA kernel over K slices, then the
+// slices' sum in slice order.
 int launch_gemm_rows_fast(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                           int64_t M, bool acc) {
-    if (w->dtype != kQ4K) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemm_rows_fast: q4_k only");
+    const int dt = w->dtype;
     const int64_t K = w->K, nb = K / 256;
-    const bool t16 = M <= F16_TM;  // one 16-row tile
-    const int64_t tiles = ((N + FM_TN - 1) / FM_TN) * (t16 ? 1 : (M + FM_TM - 1) / FM_TM);
+    if (dt != kQ4K && dt != kQ6K) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemm_rows_fast: q4_k and q6_k only");
+    const bool t16 = dt != kQ4K || M <= F16_TM;  // 16-row tiles
+    const int64_t tiles = ((N + FM_TN - 1) / FM_TN) * (t16 ? (M + F16_TM - 1) / F16_TM : (M + FM_TM - 1) / FM_TM);
     int64_t ns = (512 + tiles - 1) / tiles;  // K slices for about 512 workgroups
     if (ns > nb) ns = nb;
     const int64_t bps = (nb + ns - 1) / ns;
     ns = (nb + bps - 1) / bps;
     auto al = [](size_t v) { return (v + 255) / 256 * 256; };
     const bool copy_x = reinterpret_cast<uintptr_t>(x) % 16 != 0;
-    const size_t o_dg = 0, o_ex = al(o_dg + 3 * (size_t)(M * K)), o_xs = al(o_ex + (size_t)(M * nb) * sizeof(int));
+    // q4_k: three int8 digit planes and the f16 msum parts; q6_k: two f16 planes
+    const size_t xbytes = dt == kQ4K ? 3 * (size_t)(M * K) : 4 * (size_t)(M * K);
+    const size_t o_dg = 0, o_ex = al(o_dg + xbytes), o_xs = al(o_ex + (size_t)(M * nb) * sizeof(int));
     const size_t o_bad = al(o_xs + (size_t)(M * nb) * 48), o_x = al(o_bad + (size_t)(M * nb));
     const size_t o_p = al(o_x + (copy_x ? (size_t)(M * K) * sizeof(float) : 0));
     const size_t total = o_p + (ns > 1 ? (size_t)(ns * M * N) * sizeof(float) : 0);
@@ -828,32 +1078,45 @@ int launch_gemm_rows_fast(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, i
         xa = reinterpret_cast<const float *>(ws + o_x);
     }
     uint8_t *bad = ws + o_bad;
-    hipLaunchKernelGGL(digits_q4k_kernel, dim3((unsigned)((M * nb + 3) / 4)), dim3(256), 0, ctx->stream, xa, M, K,
-                       reinterpret_cast<int8_t *>(ws + o_dg), reinterpret_cast<int *>(ws + o_ex),
-                       reinterpret_cast<uint16_t *>(ws + o_xs), bad);
-    if ((st = launch_check(ctx, "digits_q4k")) != TRHIP_OK) return st;
+    uint16_t *xh = reinterpret_cast<uint16_t *>(ws + o_dg), *xl = xh + M * K;
+    if (dt == kQ4K)
+        hipLaunchKernelGGL(digits_q4k_kernel, dim3((unsigned)((M * nb + 3) / 4)), dim3(256), 0, ctx->stream, xa, M, K,
+                           reinterpret_cast<int8_t *>(ws + o_dg), reinterpret_cast<int *>(ws + o_ex),
+                           reinterpret_cast<uint16_t *>(ws + o_xs), bad);
+    else
+        hipLaunchKernelGGL(halves_kernel, dim3((unsigned)((M * nb + 3) / 4)), dim3(256), 0, ctx->stream, xa, M, K, xh,
+                           xl, reinterpret_cast<int *>(ws + o_ex), bad);
+    if ((st = launch_check(ctx, dt == kQ4K ? "digits_q4k" : "halves")) != TRHIP_OK) return st;
     float *partial = ns > 1 ? reinterpret_cast<float *>(ws + o_p) : nullptr;
     dim3 grid((unsigned)tiles, (unsigned)ns), block(FM_THREADS);
     const int8_t *dg = reinterpret_cast<const int8_t *>(ws + o_dg);
     const int *ex = reinterpret_cast<const int *>(ws + o_ex);
     const uint16_t *xs = reinterpret_cast<const uint16_t *>(ws + o_xs);
     const bool acc_k = acc && !partial;
-    if (t16) {  // LDS below 64 KB: no attribute needed
+    const Planes pl = w->planes();
+    if (dt == kQ6K) {
         if (acc_k)
-            hipLaunchKernelGGL(fastm16_mfma_q4k<true>, grid, block, F16_LDS, ctx->stream, w->planes(), N, row0, M, K,
-                               xa, dg, ex, xs, bad, bps, c, partial);
+            hipLaunchKernelGGL(fastm16_q6k<true>, grid, block, FH_LDS, ctx->stream, pl, N, row0, M, K, xa, xh, xl, ex,
+                               bad, bps, c, partial);
         else
-            hipLaunchKernelGGL(fastm16_mfma_q4k<false>, grid, block, F16_LDS, ctx->stream, w->planes(), N, row0, M, K,
-                               xa, dg, ex, xs, bad, bps, c, partial);
+            hipLaunchKernelGGL(fastm16_q6k<false>, grid, block, FH_LDS, ctx->stream, pl, N, row0, M, K, xa, xh, xl, ex,
+                               bad, bps, c, partial);
+    } else if (t16) {  // LDS below 64 KB: no attribute needed
+        if (acc_k)
+            hipLaunchKernelGGL(fastm16_mfma_q4k<true>, grid, block, F16_LDS, ctx->stream, pl, N, row0, M, K, xa, dg, ex,
+                               xs, bad, bps, c, partial);
+        else
+            hipLaunchKernelGGL(fastm16_mfma_q4k<false>, grid, block, F16_LDS, ctx->stream, pl, N, row0, M, K, xa, dg,
+                               ex, xs, bad, bps, c, partial);
     } else {
         if (acc_k)
-            hipLaunchKernelGGL(fastm_mfma_q4k<true>, grid, block, FM_LDS, ctx->stream, w->planes(), N, row0, M, K, xa,
-                               dg, ex, xs, bad, bps, c, partial);
+            hipLaunchKernelGGL(fastm_mfma_q4k<true>, grid, block, FM_LDS, ctx->stream, pl, N, row0, M, K, xa, dg, ex,
+                               xs, bad, bps, c, partial);
         else
-            hipLaunchKernelGGL(fastm_mfma_q4k<false>, grid, block, FM_LDS, ctx->stream, w->planes(), N, row0, M, K, xa,
-                               dg, ex, xs, bad, bps, c, partial);
+            hipLaunchKernelGGL(fastm_mfma_q4k<false>, grid, block, FM_LDS, ctx->stream, pl, N, row0, M, K, xa, dg, ex,
+                               xs, bad, bps, c, partial);
     }
-    if ((st = launch_check(ctx, "fastm_mfma_q4k")) != TRHIP_OK || !partial) return st;
+    if ((st = launch_check(ctx, "gemm_rows_fast")) != TRHIP_OK || !partial) return st;
     const int64_t MN = M * N;
     const unsigned blocks = (unsigned)((MN + 255) / 256 < 4096 ? (MN + 255) / 256 : 4096);
     if (acc)

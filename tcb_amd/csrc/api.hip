@@ -488,9 +488,9 @@ int trhip_gemm_q(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N,
         }
         return launch_gemv(ctx, w, row0, N, xa, c, accumulate != 0, mode);
     }
-    // fast mode, q4_k, M > 4: int8 matrix cores over fixed-point activations (tolerance). Up to 4 rows the exact
-    // kernel's 4-row tiles are as fast, and the other dtypes run exact.
-    if (mode == TRHIP_MODE_FAST && w->dtype == TRHIP_Q4K && M > 4)
+    // fast mode (tolerance) on matrix cores over fixed-point activations: q4_k from M = 5 (up to 4 rows the exact
+    // kernel's 4-row tiles are as fast), q6_k from M = 2; q8_0 / q4_0 run exact (their fast kernel measured slower)
+    if (mode == TRHIP_MODE_FAST && ((w->dtype == TRHIP_Q4K && M > 4) || (w->dtype == TRHIP_Q6K && M > 1)))
         return launch_gemm_rows_fast(ctx, w, row0, N, x, c, M, accumulate != 0);
     return launch_gemm_rows(ctx, w, row0, N, x, c, M, accumulate != 0);
 }
