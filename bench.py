@@ -15,10 +15,11 @@ restatement of the reference's sdotq4k path (oracle/trq_avx2.c), all host cores,
 
 Prints one JSON line. --gpus N > 1 exits: this build runs on one GPU.
 
---profile-kernel {gemv,prefill,rows,copy} runs only that kernel, eagerly, --steps times (for rocprofv3 runs):
-gemv = the headline GEMV over the cold ring, prefill = one act-quant GEMM per step, rows = one M > 1 fp32 GEMM
-(--rows-m rows, --mode exact or fast) per step, copy = a plain device copy of COPY_BYTES (torch) that calibrates
-the FETCH_SIZE / WRITE_SIZE counters.
+--profile-kernel {gemv,prefill,rows,copy,read,open_q} runs only that kernel, eagerly, --steps times (for rocprofv3
+runs): gemv = the headline GEMV over the cold ring, prefill = one act-quant GEMM per step, rows = one M > 1 fp32 GEMM
+(--rows-m rows, --rows-shape dtype,N,K, --mode exact or fast) per step, copy = a plain device copy of COPY_BYTES
+(torch) that calibrates the FETCH_SIZE / WRITE_SIZE counters, read = the streaming-read probe over a cold ring of the
+headline's bytes, open_q = OpenQuant of the headline store.
 """
 import argparse
 import json
@@ -63,9 +64,11 @@ def parse():
     ap.add_argument("--sweep", type=int, default=1, help="also time the 32-layer decode sweep (0 = skip)")
     ap.add_argument("--shapes", type=int, default=1,
                     help="also time every Llama-3-8B GEMV shape per dtype and the prefill grid (0 = skip)")
-    ap.add_argument("--profile-kernel", choices=["gemv", "prefill", "rows", "copy"], default=None,
+    ap.add_argument("--profile-kernel", choices=["gemv", "prefill", "rows", "copy", "read", "open_q"], default=None,
                     help="run only this kernel --steps times, eagerly (counter runs)")
     ap.add_argument("--rows-m", type=int, default=16, help="activation rows of --profile-kernel rows (M > 1 path)")
+    ap.add_argument("--rows-shape", default="q4_k,14336,4096",
+                    help="dtype,N,K of --profile-kernel rows (q4_k or q6_k; e.g. q6_k,128256,4096 for the output head)")
     return ap.parse_args()
 
 
@@ -288,17 +291,41 @@ def profile_kernel(a):
         print(json.dumps({"profiled": "gemv_q4_k_%s" % a.mode, "launches": a.steps,
                           "algorithmic_bytes": algorithmic_bytes(N, K)}))
     elif a.profile_kernel == "rows":
-        # the M > 1 fp32 path (batched decode): exact chunk order, or the fast int8-digit kernel with --mode fast
+        # the M > 1 fp32 path (batched decode): exact chunk order, or the fast matrix-core kernels with --mode fast
+        from tcb_amd import Q6K
         M = a.rows_m
-        w = tb.FromQuantized(Q4K, raw, N, K)
-        Xb = tb.ctx.to_device(synth.activations(M, K, seed=5))
-        Cb = tb.ctx.alloc(M * N * 4)
+        name, rn, rk = a.rows_shape.split(",")
+        rdt, rn, rk = {"q4_k": Q4K, "q6_k": Q6K}[name], int(rn), int(rk)
+        # other shapes take random-code blocks (timing only; the head's 431 MB would take minutes to encode)
+        rraw = raw if (rdt, rn, rk) == (Q4K, N, K) else synth.random_blocks(rdt, rn, rk, seed=3)
+        w = tb.FromQuantized(rdt, rraw, rn, rk)
+        Xb = tb.ctx.to_device(synth.activations(M, rk, seed=5))
+        Cb = tb.ctx.alloc(M * rn * 4)
         mode = MODE_FAST if a.mode == "fast" else MODE_EXACT
         for _ in range(a.steps):
-            tb.GemmSet(M, N, K, Xb, w, Cb, mode=mode)
+            tb.GemmSet(M, rn, rk, Xb, w, Cb, mode=mode)
         tb.ctx.sync()
-        print(json.dumps({"profiled": "rows_q4_k_%s" % a.mode, "launches": a.steps, "M": M,
-                          "algorithmic_bytes": algorithmic_bytes(N, K) + 4 * (M - 1) * (N + K)}))
+        print(json.dumps({"profiled": "rows_%s_%dx%d_%s" % (name, rn, rk, a.mode), "launches": a.steps, "M": M,
+                          "weight_bytes": int(rraw.nbytes)}))
+    elif a.profile_kernel == "read":
+        # the streaming-read ceiling: trhip_read_probe over a cold ring of plain buffers of the headline's bytes
+        nbytes = raw.nbytes // 16 * 16
+        ring = [tb.ctx.alloc(nbytes) for _ in range(max(2, -(-RING_BYTES // nbytes)))]
+        for b in ring:
+            b.fill(1)
+        for i in range(a.steps):
+            tb.ctx.read_probe(ring[i % len(ring)], nbytes)
+        tb.ctx.sync()
+        print(json.dumps({"profiled": "read_probe", "launches": a.steps, "bytes": nbytes}))
+    elif a.profile_kernel == "open_q":
+        # OpenQuant: the whole headline store dequantized to fp32
+        w = tb.FromQuantized(Q4K, raw, N, K)
+        ob = tb.ctx.alloc(N * K * 4)
+        for _ in range(a.steps):
+            tb.OpenQuant(ob, w)
+        tb.ctx.sync()
+        print(json.dumps({"profiled": "open_q_q4_k", "launches": a.steps,
+                          "bytes": int(raw.nbytes) + N * K * 4}))
     else:
         M = a.prefill_m
         w = tb.FromQuantized(Q4K, raw, N, K)
