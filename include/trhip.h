@@ -150,7 +150,9 @@ int trhip_embedding_q(trhip_ctx *ctx, const trhip_wstore *w, const int64_t *idx,
 int trhip_swiglu(trhip_ctx *ctx, const float *gu, int64_t M, int64_t I, float *out);
 
 /* SwiGLU.forward's first half on a merged store (lib/layers.tr:264-266): gu = x @ w^T over all 2I rows
- * ([gate | up], trhip_gemm_q semantics and mode), then out = trhip_swiglu(gu). out is [M, I]. */
+ * ([gate | up], trhip_gemm_q semantics and mode), then out = trhip_swiglu(gu). out is [M, I]. In fast mode
+ * with M == 1 the gate is fused into the q4_k GEMV where its K-across-lanes kernel applies (2I >= 6144, K a
+ * multiple of 256 up to 4096, 16-byte aligned x): the same bits as the two steps. */
 int trhip_gemm_q_swiglu(trhip_ctx *ctx, const trhip_wstore *w, const float *x, float *out, int64_t M,
                         int64_t K, int mode);
 

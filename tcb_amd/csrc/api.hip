@@ -513,6 +513,12 @@ int trhip_gemm_q_swiglu(trhip_ctx *ctx, const trhip_wstore *w, const float *x, f
     if (M == 0 || I == 0) return TRHIP_OK;
     if (!x || !out) return fail(ctx, TRHIP_ERR_INVALID, "gemm_q_swiglu: null x or out");
     DevGuard g(ctx);
+    // fast decode (M = 1, aligned x): the gate fused into the GEMV where its K-across-lanes kernel applies, the same
+    // bits as the two steps below
+    if (mode == TRHIP_MODE_FAST && M == 1 && K > 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0) {
+        const int r = launch_gemv_fast_swiglu(ctx, w, x, out, I);
+        if (r != -1) return r;
+    }
     int st = TRHIP_OK;
     float *gu = static_cast<float *>(workspace2(ctx, (size_t)(M * w->N) * sizeof(float), &st));
     if (!gu) return st;

@@ -281,9 +281,15 @@ struct KlRow<kQ6K> {  // ql pieces t at 32t + 16n, qh pieces at 16t + 8n, the la
     uint32_t sc, d;
 };
 
-template <int DT, bool ACC, int WAVES, int KS, int PD, int RPW>
+// SWI: the store holds 2N rows, [gate | up] (a merged gate_up layer), and c receives silu(g_i) * u_i for i < N.
+// Slots then alternate gate row i and up row N + i of the same pair; a row's sum does not depend on its slot
+// (lane_sum8 pairs the same lanes for every slot), so the outputs are the unfused GEMV's sums gated exactly as
+// swiglu_kernel gates them.
+template <int DT, bool ACC, int WAVES, int KS, int PD, int RPW, bool SWI = false>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const float *__restrict__ x,
                                                       float *__restrict__ c, int64_t N, int64_t row0) {
+    static_assert(!(SWI && ACC), "the gated output is set, not accumulated");
+    static_assert(!SWI || RPW % 2 == 0, "slots come in gate / up pairs");
     constexpr int RG = WAVES / KS;
     static_assert(16 % RG == 0, "the row groups of a part split the 16 columns of x evenly");
     static_assert(RPW % PD == 0, "rows are consumed PD at a time from a ring of PD slots");
@@ -347,11 +353,19 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const floa
         }
     };
     (void)QW;
-    // row counts fit 32 bits (the launcher checks), so the uniform row arithmetic stays 32-bit
+    // row counts fit 32 bits (the launcher checks), so the uniform row arithmetic stays 32-bit. Without SWI slot i is
+    // output row gw + i G; with SWI, slots 2j and 2j + 1 are gate row gw + j G and up row N + gw + j G
     const uint32_t G = gridDim.x * RG, gw = blockIdx.x * RG + rg, n32 = (uint32_t)N;
-    const uint32_t nv = gw < n32 ? (n32 - 1 - gw) / G + 1 : 0;                 // rows of this row group
+    const uint32_t nv = gw < n32 ? (n32 - 1 - gw) / G + 1 : 0;                 // outputs of this row group
     const uint32_t last = nv > 0 ? gw + (nv - 1) * G : gw - (gw / n32) * n32;  // what slots past them re-read
-    auto row_of = [&](int i) { return row0 + (int64_t)((uint32_t)i < nv ? gw + (uint32_t)i * G : last); };
+    auto row_of = [&](int i) {
+        if constexpr (SWI) {
+            const uint32_t j = (uint32_t)i >> 1, o = j < nv ? gw + j * G : last;
+            return row0 + (int64_t)o + ((i & 1) ? N : 0);
+        } else {
+            return row0 + (int64_t)((uint32_t)i < nv ? gw + (uint32_t)i * G : last);
+        }
+    };
     KlRow<DT> R[PD];
 #pragma unroll
     for (int s = 0; s < PD; s++) load_row(R[s], row_of(s));
@@ -594,8 +608,14 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const floa
                 for (int q = 1; q < KS; q++) sum = sum + pl[((q - 1) * RG + rg) * 8 + ri];
             }
         }
-        const int64_t r = gw + (int64_t)(i0 + ri) * G;
-        if (part == 0 && (lane & 7) == 0 && (uint32_t)(i0 + ri) < nv) c[r] = ACC ? c[r] + sum : sum;
+        if constexpr (SWI) {  // rows ri (even: gate) and ri + 1 (up) of the eight are lanes 8 ri and 8 ri + 8
+            const float up = __shfl_xor(sum, 8);
+            const uint32_t j = (uint32_t)(i0 + ri) >> 1;
+            if (part == 0 && (lane & 15) == 0 && j < nv) c[gw + (int64_t)j * G] = silu_ref(sum) * up;
+        } else {
+            const int64_t r = gw + (int64_t)(i0 + ri) * G;
+            if (part == 0 && (lane & 7) == 0 && (uint32_t)(i0 + ri) < nv) c[r] = ACC ? c[r] + sum : sum;
+        }
     }
 }
 
@@ -606,14 +626,20 @@ __host__ __forceinline__ bool kl_fits(int dt, int64_t nb, int ks) {
     return nb % 2 == 0 && ((nb + ks - 1) / ks + 1) / 2 * 2 <= 128;
 }
 
-template <int DT, int WAVES, int KS, int PD, int RPW>
+template <int DT, int WAVES, int KS, int PD, int RPW, bool SWI = false>
 int run_kl(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c, bool acc) {
     constexpr int RG = WAVES / KS;
     if (!kl_fits(DT, w->nb, KS)) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv_kl: K parts too long for the lanes of a wave");
-    const int64_t wgs = (N + RG * RPW - 1) / (RG * RPW);  // every row group gets at most RPW rows
-    if (N >= (int64_t)1 << 31 || wgs * RG >= (int64_t)1 << 31)
-        return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv_kl: more than 2^31 rows");
+    constexpr int OPW = SWI ? RPW / 2 : RPW;  // outputs per row group (SWI: two rows per output)
+    const int64_t wgs = (N + RG * OPW - 1) / (RG * OPW);  // every row group gets at most RPW rows
+    if (N >= (int64_t)1 << 30 || wgs * RG >= (int64_t)1 << 31)
+        return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv_kl: more than 2^30 rows");
     dim3 grid((unsigned)wgs), block(64 * WAVES);
+    if constexpr (SWI) {
+        hipLaunchKernelGGL((gemv_kl<DT, false, WAVES, KS, PD, RPW, true>), grid, block, 0, ctx->stream, w->planes(), x, c,
+                           N, row0);
+        return launch_check(ctx, "gemv_kl_swiglu");
+    }
     if (acc)
         hipLaunchKernelGGL((gemv_kl<DT, true, WAVES, KS, PD, RPW>), grid, block, 0, ctx->stream, w->planes(), x, c, N, row0);
     else
@@ -690,6 +716,16 @@ int kl_q6k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const
     return kNotTaken;
 }
 }  // namespace
+
+// q4_k GEMV with the SwiGLU gate fused (merged [gate | up] store of 2I rows, M = 1): the K-across-lanes launch
+// shape the unfused fast GEMV takes for 2I rows, so every row sum, and so every gated output, has the same bits
+int launch_gemv_fast_swiglu(trhip_ctx *ctx, const trhip_wstore *w, const float *x, float *out, int64_t I) {
+    const int64_t N2 = 2 * I;
+    if (w->dtype != kQ4K || w->N != N2 || getenv("TRHIP_KL") || w->nb < 8 || w->nb > 16) return kNotTaken;
+    if (N2 >= 10240) return run_kl<kQ4K, 4, 1, 4, 16, true>(ctx, w, 0, I, x, out, false);
+    if (N2 >= 6144) return run_kl<kQ4K, 4, 1, 4, 8, true>(ctx, w, 0, I, x, out, false);
+    return kNotTaken;
+}
 
 int launch_gemv_fast(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                      bool acc) {

@@ -119,6 +119,38 @@ __device__ __forceinline__ float deq_at(const Planes p, int64_t row, int64_t k) 
     }
 }
 
+// silu(x) = x sigma(x) as TR's siluForward (tensor/cpu_elementwise_wide.go:101-116, sigmoidBlock :83-98) with e^x
+// the AVX2 expVec it runs for every element (tensor/cpu_vector_amd64.s:13-38): clamp to [-104, 89] (NaN takes the
+// lower bound and is put back at the end), n = rne(x log2e), r = x - n ln2 in two fused steps (ln2 split high/low),
+// a degree-6 polynomial in fused steps, and 2^n applied as 2^(n>>1) * 2^(n - n>>1), so subnormal results and
+// overflow to +Inf come out right. Same operations in the same order (files are built with -ffp-contract=off).
+__device__ __forceinline__ float exp_ref(float x) {
+    float x1 = x > -104.0f ? x : -104.0f;
+    x1 = x1 < 89.0f ? x1 : 89.0f;
+    const float n = __builtin_rintf(x1 * 1.44269504088896341f);
+    float r = __builtin_fmaf(-n, 0.693359375f, x1);
+    r = __builtin_fmaf(-n, -2.12194440e-4f, r);
+    float p = 1.9875691500e-4f;
+    p = __builtin_fmaf(p, r, 1.3981999507e-3f);
+    p = __builtin_fmaf(p, r, 8.3334519073e-3f);
+    p = __builtin_fmaf(p, r, 4.1665795894e-2f);
+    p = __builtin_fmaf(p, r, 1.6666665459e-1f);
+    p = __builtin_fmaf(p, r, 5.0000001201e-1f);
+    const float z = r * r;
+    p = __builtin_fmaf(z, p, r);
+    float y = p + 1.0f;
+    const int ni = (int)n, h = ni >> 1, l = ni - h;
+    y = y * __builtin_bit_cast(float, (uint32_t)(h + 127) << 23);
+    y = y * __builtin_bit_cast(float, (uint32_t)(l + 127) << 23);
+    return x != x ? x : y;
+}
+// x sigma(x) with e = e^-|x|: sigma = 1/(1+e) for x >= 0, e/(1+e) otherwise; sigma == 0 gives +0.
+__device__ __forceinline__ float silu_ref(float x) {
+    const float e = exp_ref(-__builtin_fabsf(x));
+    const float s = x >= 0.0f ? 1.0f / (1.0f + e) : e / (1.0f + e);
+    return (s == 0.0f ? 0.0f : x) * s;
+}
+
 // Exact fp32 dot of activation row xr with weight row `row` in sdot32 order (fallback for rows with
 // NaN/Inf; one thread, 32 chains).
 template <int DT>
@@ -181,6 +213,10 @@ int launch_embedding(trhip_ctx *ctx, const trhip_wstore *w, const int64_t *idx, 
                      int *bad_dev);
 int launch_gemv(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                 bool acc, int mode);
+// Fast-mode GEMV over a merged [gate | up] store of 2I rows with the SwiGLU gate fused: out[i] = silu(g_i) * u_i,
+// bit-identical to the fast GEMV followed by launch_swiglu. Returns -1 (nothing launched) where the fused kernel
+// does not apply.
+int launch_gemv_fast_swiglu(trhip_ctx *ctx, const trhip_wstore *w, const float *x, float *out, int64_t I);
 int launch_gemm_rows(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                      int64_t M, bool acc);
 int launch_gemm_rows_fast(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,

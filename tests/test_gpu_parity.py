@@ -668,6 +668,29 @@ def test_gemm_q_swiglu_bits(backend, dt, M):
         p.release()
 
 
+@pytest.mark.parametrize("I,K", [(3100, 4096), (5120, 4096), (14336, 4096), (3100, 2048)])
+def test_gemm_q_swiglu_fused_fast(backend, I, K):
+    """Fast decode with the SwiGLU gate fused into the q4_k GEMV (merged [gate | up] stores of 6144 or more rows):
+    the same bits as the fast GEMV over the merged store followed by swiglu_gate, for an aligned and an unaligned x
+    (the latter takes the two-step path); the GEMV within the q4_k bound of the exact one."""
+    raw = synth.quant_weights(Q4K, 2 * I, K, seed=I + K, outliers=0.01)
+    w = backend.FromQuantized(Q4K, raw, 2 * I, K)
+    x = synth.activations(1, K, seed=K + 1)
+    xb = backend.ctx.alloc(K * 4 + 64)
+    gub, ob = backend.ctx.alloc(2 * I * 4), backend.ctx.alloc(I * 4)
+    for off in (0, 4):
+        xb.upload(x, byte_offset=off)
+        backend.GemmSet(1, 2 * I, K, (xb, off), w, gub, mode=MODE_FAST)
+        gu = gub.download(np.float32, 2 * I)
+        backend.GemmSwiGLU(1, K, (xb, off), w, ob, mode=MODE_FAST)
+        same_bits(ob.download(np.float32, I), O.swiglu(gu.reshape(1, 2 * I), 1, I).reshape(-1))
+    want = O.quant_gemm(Q4K, 1, 2 * I, K, x, raw).reshape(-1)
+    assert rel_err(gu, want) <= FAST_TOL[Q4K]
+    for b in (xb, gub, ob):
+        b.free()
+    w.release()
+
+
 FASTM_SHAPES = [(5, 100, 256, 0), (8, 300, 4096, 5), (16, 1000, 4096, 0), (17, 129, 3840, 3), (33, 70, 14336, 0),
                 (64, 9000, 4096, 0)]
 
