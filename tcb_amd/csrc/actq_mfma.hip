@@ -292,13 +292,14 @@ int run_mfma(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, con
 //
 // The reference's GPU backend runs M > 1 as dequantized tiles through a float GEMM (gpu/backend_quant.go:43-134):
 // a tolerance path. Here each 256-wide block b of activation row m is put on a fixed-point grid,
-//   E = exponent of max|x| (max|x| < 2^E),  X_i = rint(x_i 2^(20-E)),  |X_i| <= 2^20,
-//   X = D0 + 128 D1 + 16384 D2  with balanced digits D0, D1 in [-64, 63], D2 in [-64, 64],
+//   max|x| = f 2^E (f in [0.5, 1), E one higher when f > 127/128),  X_i = rint(x_i 2^(23-E)),  |X_i| <= 127 2^16,
+//   X = D0 + 256 D1 + 65536 D2  with balanced digits D0, D1 in [-128, 127] and D2 in [-128, 127],
 // so that with q4_k weights y = d sc_j q - dmin m_j,
-//   sum_i x_i y_i ~= 2^(E-20) (d isum - dmin msum),
-//   isum = sum_t 128^t sum_i (sc q)_i D_t,i    three int8 MFMA accumulations per scale half, exact in int32,
-//   msum = sum_j m_j XS_j,  XS_j = sum_{i in j} X_i = P0 + 512 P1 + 2^18 P2 (f16-exact parts), one f16 MFMA
-// pair. The only rounding besides the 2^-21 grid is the fp32 epilogue, within the 1e-4 tolerance of the fast mode.
+//   sum_i x_i y_i ~= 2^(E-23) (d isum - dmin msum),
+//   isum = sum_t 256^t sum_i (sc q)_i D_t,i    three int8 MFMA accumulations per scale half, exact in int32,
+//   msum = sum_j m_j XS_j,  XS_j = sum_{i in j} X_i = P0 + 512 P1 + 2^18 P2 (f16-exact parts, |P2| <= 1016), one
+// f16 MFMA pair. Besides the grid (2^-23 to 2^-22 of the block's largest |x|) only the fp32 epilogue rounds, within
+// the 1e-4 tolerance of the fast mode.
 // Rows holding NaN/Inf are computed with exact float dot products instead, as the act-quant path does.
 
 constexpr int FM_TM = 32, FM_TN = 128, FM_THREADS = 256;
@@ -329,16 +330,16 @@ __global__ __launch_bounds__(256) void digits_q4k_kernel(const float *__restrict
     for (int o = 1; o < 64; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
     const bool allfin = __all(fin);
     int E = 0;
-    if (allfin && amax > 0.0f) frexpf(amax, &E);
+    if (allfin && amax > 0.0f && frexpf(amax, &E) > 127.0f / 128.0f) E += 1;  // keeps |X| <= 127 2^16
     const float xv[4] = {v.x, v.y, v.z, v.w};
     int X[4];
     uint32_t d0 = 0, d1 = 0, d2 = 0;
     int xs = 0;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        X[i] = allfin ? (int)rintf(ldexpf(xv[i], 20 - E)) : 0;
-        const int a0 = ((X[i] + 64) & 127) - 64, r1 = (X[i] - a0) >> 7;
-        const int a1 = ((r1 + 64) & 127) - 64, a2 = (r1 - a1) >> 7;
+        X[i] = allfin ? (int)rintf(ldexpf(xv[i], 23 - E)) : 0;
+        const int a0 = (int)(int8_t)(X[i] & 0xFF), r1 = (X[i] - a0) >> 8;
+        const int a1 = (int)(int8_t)(r1 & 0xFF), a2 = (r1 - a1) >> 8;
         d0 |= (uint32_t)(a0 & 0xFF) << (8 * i);
         d1 |= (uint32_t)(a1 & 0xFF) << (8 * i);
         d2 |= (uint32_t)(a2 & 0xFF) << (8 * i);
@@ -361,7 +362,7 @@ __global__ __launch_bounds__(256) void digits_q4k_kernel(const float *__restrict
         o[16 + j] = __builtin_bit_cast(uint16_t, (_Float16)(float)p2);
     }
     if (lane == 0) {
-        ex[m * nb + b] = E - 20;
+        ex[m * nb + b] = E - 23;
         bad[m * nb + b] = allfin ? 0 : 1;
     }
 }
@@ -484,7 +485,7 @@ __global__ __launch_bounds__(FM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
         for (int v = 0; v < 16; v++) {
             const float f0 = (float)(c0[0][v] + 8 * c1[0][v]), f1 = (float)(c0[1][v] + 8 * c1[1][v]),
                         f2 = (float)(c0[2][v] + 8 * c1[2][v]);
-            fs[v] = fmaf(16384.0f, f2, fmaf(128.0f, f1, f0));
+            fs[v] = fmaf(65536.0f, f2, fmaf(256.0f, f1, f0));
         }
         if (b + 1 < b1) {
             put_a((b + 1 - b0) & 1);
@@ -700,7 +701,7 @@ __global__ __launch_bounds__(FM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
             for (int v = 0; v < 4; v++) {
                 const float f0 = (float)(c0[t][0][v] + 8 * c1[t][0][v]), f1 = (float)(c0[t][1][v] + 8 * c1[t][1][v]),
                             f2 = (float)(c0[t][2][v] + 8 * c1[t][2][v]);
-                fs[t][v] = fmaf(16384.0f, f2, fmaf(128.0f, f1, f0));
+                fs[t][v] = fmaf(65536.0f, f2, fmaf(256.0f, f1, f0));
             }
         if (b + 1 < b1) {
             put_a((b + 1 - b0) & 1);
@@ -1024,6 +1025,32 @@ __global__ __launch_bounds__(FM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
     }
 }
 
+// out[m, i] = silu(g) * u with g, u the slice sums of partial rows i and I + i of activation row m, each added in
+// slice order as fm_sum_kernel adds them: the same bits as fm_sum_kernel followed by swiglu_kernel.
+__global__ void fm_sum_swiglu_kernel(const float *__restrict__ partial, float *__restrict__ out, int64_t M, int64_t I,
+                                     int64_t ns) {
+    const int64_t N = 2 * I, MN = M * N;
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < M * I; t += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t m = t / I, i = t - m * I, og = m * N + i, ou = og + I;
+        float g = partial[og], u = partial[ou];
+        for (int64_t k = 1; k < ns; k += 4) {  // up to eight loads in flight, added in slice order
+            float vg[4], vu[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                vg[q] = k + q < ns ? partial[(k + q) * MN + og] : 0.0f;
+                vu[q] = k + q < ns ? partial[(k + q) * MN + ou] : 0.0f;
+            }
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                if (k + q < ns) {
+                    g = g + vg[q];
+                    u = u + vu[q];
+                }
+        }
+        out[t] = silu_ref(g) * u;
+    }
+}
+
 }  // namespace
 
 int launch_actq_mfma(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
@@ -1050,7 +1077,7 @@ namespace trhip {
 // fastm16_mfma_q4k; q6_k: two f16 planes for fastm16_q6k on 16-row tiles), the MFMA kernel over K slices, then the
 // slices' sum in slice order.
 int launch_gemm_rows_fast(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
-                          int64_t M, bool acc) {
+                          int64_t M, bool acc, float *swi) {
     const int dt = w->dtype;
     const int64_t K = w->K, nb = K / 256;
     if (dt != kQ4K && dt != kQ6K) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemm_rows_fast: q4_k and q6_k only");
@@ -1116,7 +1143,15 @@ int launch_gemm_rows_fast(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, i
             hipLaunchKernelGGL(fastm_mfma_q4k<false>, grid, block, FM_LDS, ctx->stream, pl, N, row0, M, K, xa, dg, ex,
                                xs, bad, bps, c, partial);
     }
-    if ((st = launch_check(ctx, "gemm_rows_fast")) != TRHIP_OK || !partial) return st;
+    if ((st = launch_check(ctx, "gemm_rows_fast")) != TRHIP_OK) return st;
+    if (swi) {  // SwiGLU gate over [gate | up] = N = 2I columns, fused into the slice sum
+        if (!partial) return launch_swiglu(ctx, c, M, N / 2, swi);
+        const int64_t MI = M * (N / 2);
+        const unsigned blocks = (unsigned)((MI + 255) / 256 < 4096 ? (MI + 255) / 256 : 4096);
+        hipLaunchKernelGGL(fm_sum_swiglu_kernel, dim3(blocks), dim3(256), 0, ctx->stream, partial, swi, M, N / 2, ns);
+        return launch_check(ctx, "fm_sum_swiglu");
+    }
+    if (!partial) return st;
     const int64_t MN = M * N;
     const unsigned blocks = (unsigned)((MN + 255) / 256 < 4096 ? (MN + 255) / 256 : 4096);
     if (acc)

@@ -522,6 +522,9 @@ int trhip_gemm_q_swiglu(trhip_ctx *ctx, const trhip_wstore *w, const float *x, f
     int st = TRHIP_OK;
     float *gu = static_cast<float *>(workspace2(ctx, (size_t)(M * w->N) * sizeof(float), &st));
     if (!gu) return st;
+    // fast M > 1 on matrix cores (as trhip_gemm_q dispatches it): the gate fused into the K-slice sum
+    if (mode == TRHIP_MODE_FAST && K > 0 && ((w->dtype == TRHIP_Q4K && M > 4) || (w->dtype == TRHIP_Q6K && M > 1)))
+        return launch_gemm_rows_fast(ctx, w, 0, w->N, x, gu, M, false, out);
     if ((st = trhip_gemm_q(ctx, w, 0, w->N, x, gu, M, K, 0, mode)) != TRHIP_OK) return st;
     return launch_swiglu(ctx, gu, M, I, out);
 }

@@ -219,8 +219,10 @@ int launch_gemv(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, 
 int launch_gemv_fast_swiglu(trhip_ctx *ctx, const trhip_wstore *w, const float *x, float *out, int64_t I);
 int launch_gemm_rows(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                      int64_t M, bool acc);
+// swi != nullptr (set, not accumulate; N = 2I rows [gate | up]): out swi[m, i] = silu(c[m, i]) * c[m, I + i], fused
+// into the slice sum when K is split (c is then not written), else after it
 int launch_gemm_rows_fast(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
-                          int64_t M, bool acc);
+                          int64_t M, bool acc, float *swi = nullptr);
 int launch_quantize_q8(trhip_ctx *ctx, const float *x, int64_t M, int64_t K, int blk, int8_t *q, float *d,
                        int16_t *bs, uint8_t *bad, uint16_t *sj);
 int launch_read_probe(trhip_ctx *ctx, const void *p, int64_t bytes);

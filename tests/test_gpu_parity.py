@@ -651,14 +651,14 @@ def test_gemm_q_swiglu_bits(backend, dt, M):
     gu = np.concatenate([O.quant_gemm(dt, M, I, K, x, graw), O.quant_gemm(dt, M, I, K, x, uraw)], axis=1)
     want = O.swiglu(gu, M, I).reshape(-1)
     same_bits(ob.download(np.float32, M * I), want)
-    if M == 1:
-        gub = backend.ctx.alloc(2 * I * 4)
-        backend.GemmSet(1, 2 * I, K, xb, w, gub, mode=MODE_FAST)
-        gu_fast = gub.download(np.float32, 2 * I)
-        assert rel_err(gu_fast, gu.reshape(-1)) <= FAST_TOL[dt]
-        backend.GemmSwiGLU(M, K, xb, w, ob, mode=MODE_FAST)
-        same_bits(ob.download(np.float32, M * I), O.swiglu(gu_fast.reshape(1, 2 * I), M, I).reshape(-1))
-        gub.free()
+    # fast mode (M > 1 on matrix cores: the gate fused into the K-slice sum)
+    gub = backend.ctx.alloc(M * 2 * I * 4)
+    backend.GemmSet(M, 2 * I, K, xb, w, gub, mode=MODE_FAST)
+    gu_fast = gub.download(np.float32, M * 2 * I)
+    assert rel_err(gu_fast, gu.reshape(-1)) <= FAST_TOL[dt]
+    backend.GemmSwiGLU(M, K, xb, w, ob, mode=MODE_FAST)
+    same_bits(ob.download(np.float32, M * I), O.swiglu(gu_fast.reshape(M, 2 * I), M, I).reshape(-1))
+    gub.free()
     odd = backend.FromQuantized(dt, _weights(dt, 3, K, 1), 3, K)
     with pytest.raises(TrhipError):
         backend.GemmSwiGLU(M, K, xb, odd, ob)
@@ -666,6 +666,24 @@ def test_gemm_q_swiglu_bits(backend, dt, M):
         b.free()
     for p in (wg, wu, w, odd):
         p.release()
+
+
+@pytest.mark.parametrize("dt", [Q4K, Q6K])
+@pytest.mark.parametrize("M,I,K", [(16, 300, 256), (16, 1000, 4096), (8, 700, 2048)])
+def test_gemm_q_swiglu_fast_rows(backend, dt, M, I, K):
+    """Fast M > 1: the gate fused into the K-slice sum (or applied after the kernel when K is one slice) gives
+    the bits of the fast GEMM followed by swiglu_gate."""
+    raw = synth.quant_weights(dt, 2 * I, K, seed=I + M, outliers=0.01)
+    w = backend.FromQuantized(dt, raw, 2 * I, K)
+    X = synth.activations(M, K, seed=K + M)
+    xb, gub, ob = backend.ctx.to_device(X), backend.ctx.alloc(M * 2 * I * 4), backend.ctx.alloc(M * I * 4)
+    backend.GemmSet(M, 2 * I, K, xb, w, gub, mode=MODE_FAST)
+    gu = gub.download(np.float32, M * 2 * I).reshape(M, 2 * I)
+    backend.GemmSwiGLU(M, K, xb, w, ob, mode=MODE_FAST)
+    same_bits(ob.download(np.float32, M * I), O.swiglu(gu, M, I).reshape(-1))
+    for b in (xb, gub, ob):
+        b.free()
+    w.release()
 
 
 @pytest.mark.parametrize("I,K", [(3100, 4096), (5120, 4096), (14336, 4096), (3100, 2048)])
