@@ -214,15 +214,15 @@ __device__ __forceinline__ float lane_sum8(float v[8], int lane) {
     return a;
 }
 
-// Fixed-point x for v_dot4_i32_i8: within a 32-element half with 2^e > max|x|, X = rint(x * 2^(22-e)), so
-// |X| <= 2^22, split into signed bytes X = d2*2^16 + d1*2^8 + d0 (d0, d1 in [-128, 127], |d2| <= 65). x4_digits
-// packs the digits of four consecutive elements into three dwords (digit t of element k in byte k of
-// dword t); one unit of X weighs 2^(e-22).
+// Fixed-point x for v_dot4_i32_i8: within a 32-element half, X = rint(x * 2^(23-e)) with e from grid_exp, so
+// |X| <= 2^23 * 127/128, split into signed bytes X = d2*2^16 + d1*2^8 + d0 (d0, d1 in [-128, 127], |d2| <= 127).
+// x4_digits packs the digits of four consecutive elements into three dwords (digit t of element k in byte k of
+// dword t); one unit of X weighs 2^(e-23).
 __device__ __forceinline__ void x4_digits(const float *xv, int e, uint32_t out[3]) {
     uint32_t p0 = 0, p1 = 0, p2 = 0;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-        const int X = (int)rintf(ldexpf(xv[k], 22 - e));
+        const int X = (int)rintf(ldexpf(xv[k], 23 - e));
         const int d0 = (int)(int8_t)(X & 0xFF), x1 = (X - d0) >> 8;
         const int d1 = (int)(int8_t)(x1 & 0xFF), d2 = (x1 - d1) >> 8;
         p0 |= (uint32_t)(d0 & 0xFF) << (8 * k);
@@ -234,12 +234,20 @@ __device__ __forceinline__ void x4_digits(const float *xv, int e, uint32_t out[3
     out[2] = p2;
 }
 
+// Exponent of a half's grid: m = f * 2^e with f in [0.5, 1) (0 gives e = 0), raised by one when f > 127/128, so
+// that |x| * 2^(23-e) <= 2^23 * 127/128 and the top digit stays a signed byte.
+__device__ __forceinline__ int grid_exp(float m) {
+    int e = 0;
+    const float f = frexpf(m, &e);
+    return f > 127.0f / 128.0f ? e + 1 : e;
+}
+
 // q4_k, K across lanes. A K part is up to 16 blocks; lane l of a wave owns quarter g = l & 3 of block l >> 2 of
 // its part: qs bytes 32g .. 32g+31 (the low nibbles are sub-block 2g, the high nibbles sub-block 2g+1), i.e. the
 // 64 contiguous elements 256b + 64g .. +63. Their x stays in registers for the whole kernel as fixed-point digits
 // (x4_digits), so the products with the 4-bit codes are exact integer dot products (v_dot4_i32_i8, one per digit
 // and four codes) and only the per-sub-block sums are rounded:
-//   sum_e y_e x_e = s_j * 2^(e-22) * (sum_e q_e X_e) - m_j * (sum_e x_e).
+//   sum_e y_e x_e = s_j * 2^(e-23) * (sum_e q_e X_e) - m_j * (sum_e x_e).
 // The fixed-point x is exact to 2^-23 of the largest |x| of its 32-element half; a lane whose x holds Inf or NaN
 // (or whose x sums overflow) takes float products of the dequantized values instead (IEEE propagation).
 //
@@ -255,8 +263,8 @@ __device__ __forceinline__ void x4_digits(const float *xv, int e, uint32_t out[3
 // digits and row streaming: lane l owns blocks 2l and 2l + 1 of its part (up to 128 blocks), which are the same
 // 64 contiguous elements, one block per 32-element half. q8_0: the codes are signed bytes, four per v_dot4;
 // q4_0: byte j of a block holds elements j (low nibble) and j + 16 (high nibble), so the low nibbles meet digit
-// words 0..3 of the half and the high nibbles words 4..7. Per block, sum_e y_e x_e = d * 2^(e-22) * sum_e q_e X_e
-// (q8_0) or d * (2^(e-22) * sum_e q_e X_e - 8 * sum_e x_e) (q4_0).
+// words 0..3 of the half and the high nibbles words 4..7. Per block, sum_e y_e x_e = d * 2^(e-23) * sum_e q_e X_e
+// (q8_0) or d * (2^(e-23) * sum_e q_e X_e - 8 * sum_e x_e) (q4_0).
 template <int DT>
 struct KlRow;  // one row slot: the bytes a lane reads for its 64 elements
 
@@ -400,11 +408,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const floa
             m0 = fmaxf(m0, t.z);
             m1 = fmaxf(m1, t.w);
         }
-        int e0 = 0, e1 = 0;
-        (void)frexpf(m0, &e0);  // m = f * 2^e, f in [0.5, 1); 0 gives e = 0
-        (void)frexpf(m1, &e1);
-        ex[0] = e0 - 22;
-        ex[1] = e1 - 22;
+        const int e0 = grid_exp(m0), e1 = grid_exp(m1);
+        ex[0] = e0 - 23;
+        ex[1] = e1 - 23;
 #pragma unroll
         for (int i = 0; i < CPW; i++) {
             const int col = rg * CPW + i;

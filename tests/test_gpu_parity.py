@@ -709,6 +709,37 @@ def test_gemm_q_swiglu_fused_fast(backend, I, K):
     w.release()
 
 
+@pytest.mark.parametrize("dt", DTS)
+@pytest.mark.parametrize("M", [1, 16])
+@pytest.mark.parametrize("N,K", [(300, 1024), (6144, 4096), (700, 14336), (10240, 2048)])
+def test_fast_random_scale_blocks(backend, dt, M, N, K):
+    """Every fast kernel (the M = 1 GEMVs, both q4_k layouts, and the M > 1 matrix-core paths) on TR's random
+    blocks with moderate random scales (cpu_quant_test.go:71-86), x ~ N(0, 1).
+
+    Such rows cancel: sum |w x| is 10^3 to 10^5 times |y|, so the exact fp32 sum is itself 1e-5 to 5e-4 away
+    from the float64 value of the same product, and no other summation order can stay within 1e-5 of its
+    rounding. Two bounds are checked: the reference's own GPU-against-CPU rule for these blocks,
+    |a - b| / (1 + |b|) <= 1e-5 sqrt(K) (gpu/behavior_quant_test.go:298, :395); and against the float64 product,
+    the fast result is no further than the dtype's bound or twice the exact path's own distance, whichever is
+    larger. (The fixed-point grid error, about rms(w) 2^-23 max|x| sqrt(K), is the same order as the fp32
+    rounding of the exact sum here; the measured ratio of the two distances is 0.4 to 1.05.)"""
+    raw = _weights(dt, N, K, N + K + M)
+    w = backend.FromQuantized(dt, raw, N, K)
+    X = _x(_rng(M + K), M * K).reshape(M, K)
+    xb, cb = backend.ctx.to_device(X), backend.ctx.alloc(M * N * 4)
+    backend.GemmSet(M, N, K, xb, w, cb, mode=MODE_FAST)
+    got = cb.download(np.float32, M * N)
+    exact = O.quant_gemm(dt, M, N, K, X, raw).reshape(-1)
+    err = rel_err(got, exact)
+    assert err <= 1e-5 * np.sqrt(K), (dt, M, N, K, err)
+    truth = (X.astype(np.float64) @ O.dequant(dt, raw).reshape(N, K).astype(np.float64).T).reshape(-1)
+    fast_err, exact_err = rel_err(got, truth), rel_err(exact, truth)
+    assert fast_err <= max(FAST_TOL[dt], 2.0 * exact_err), (dt, M, N, K, fast_err, exact_err)
+    for b in (xb, cb):
+        b.free()
+    w.release()
+
+
 FASTM_SHAPES = [(5, 100, 256, 0), (8, 300, 4096, 5), (16, 1000, 4096, 0), (17, 129, 3840, 3), (33, 70, 14336, 0),
                 (64, 9000, 4096, 0)]
 
