@@ -13,7 +13,7 @@ Also reported: the act-quant prefill GEMM (Q4_K 14336 x 4096, M = 512 rows quant
 device, int32 block sums, fp32 epilogue) in int8 TOPS = 2*M*N*K / time, and the CPU baseline: the AVX2
 restatement of the reference's sdotq4k path (oracle/trq_avx2.c), all host cores, on the same bytes.
 
-Prints one JSON line. --gpus N > 1 exits: this build runs on one GPU.
+Prints one JSON line. --gpus N > 1 exits: the measurement covers one GPU.
 
 --profile-kernel {gemv,prefill,rows,copy,read,open_q} runs only that kernel, eagerly, --steps times (for rocprofv3
 runs): gemv = the headline GEMV over the cold ring, prefill = one act-quant GEMM per step, rows = one M > 1 fp32 GEMM
@@ -162,9 +162,9 @@ def decode_sweep(tb, batches, mode, replays=5):
 
 
 def shape_table(tb):
-    """Cold-ring GEMV time for every Llama-3-8B linear shape and dtype (exact and fast), the M > 1 path at the
-    configs' batch sizes, OpenQuant and the quantized embedding lookup, and the prefill grid M in {128, 512, 2048} x both FFN shapes. Random-code blocks
-    (synth.random_blocks): timing only."""
+    """Cold-ring GEMV time for every Llama-3-8B linear shape and dtype (exact and fast), the M > 1 path at batch
+    8 (q4_0) and 16 (q4_k, q6_k head), OpenQuant and the quantized embedding lookup, and the prefill grid
+    M in {128, 512, 2048} x both FFN shapes. Random-code blocks (synth.random_blocks): timing only."""
     from tcb_amd import MODE_EXACT, MODE_FAST, Q4, Q4K, Q6K, Q8, _lib, synth
     L = _lib.lib()
     ctx = tb.ctx
@@ -375,7 +375,7 @@ def capture(tb, body):
 def main():
     a = parse()
     if a.gpus != 1:
-        print("bench.py: this build measures one MI355X; multi-GPU runs (--gpus %d) are not part of it." % a.gpus,
+        print("bench.py: measures one MI355X; multi-GPU runs (--gpus %d) are not supported." % a.gpus,
               file=sys.stderr)
         return 2
     if a.profile_kernel:

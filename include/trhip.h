@@ -43,7 +43,8 @@ enum { TRHIP_Q8 = 1, TRHIP_Q4 = 2, TRHIP_Q4K = 3, TRHIP_Q6K = 4 };
 
 /* GEMV arithmetic for fp32 activations (trhip_gemm_q with M == 1).
  * EXACT: bit-identical to TR's CPU quantDot (dequant + sdot32 order).
- * FAST:  per-sub-block factored sums; within the north-star tolerance, not bit-identical. */
+ * FAST:  per-sub-block factored sums; within 1e-5 (q8_0, q4_0) or 1e-4 (q4_k, q6_k) of EXACT by
+ *        |a - b| / (1 + |b|), not bit-identical. */
 enum { TRHIP_MODE_EXACT = 0, TRHIP_MODE_FAST = 1 };
 
 typedef struct trhip_ctx trhip_ctx;

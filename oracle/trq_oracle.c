@@ -6,7 +6,7 @@
  * places where the reference's assembly uses VFMADD231PS / VFMSUB213PS.
  *
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use this code, and
- * only as the checker or the timed CPU baseline; the product library never calls it.
+ * only as the expected result or the timed CPU baseline; the product library never calls it.
  */
 #include "trq_oracle.h"
 

@@ -2,7 +2,7 @@
  * trq_oracle.h -- CPU oracle for TR's quantized GGUF matmul (test infrastructure only).
  *
  * This is a plain-C restatement of the reference's CPU algorithm, used ONLY as the
- * parity checker by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg.
+ * expected result of the parity tests (tests/), __graft_entry__.smoke() and bench.py's cpu_baseline leg.
  * The product (libtrhip) never links, loads or calls it.
  *
  * Every function cites the reference file:line it restates (paths relative to the

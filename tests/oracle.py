@@ -1,4 +1,4 @@
-"""ctypes view of the CPU oracle (oracle/liboracle.so) for the tests: checker only."""
+"""ctypes view of the CPU oracle (oracle/liboracle.so) for the tests: expected results only."""
 import ctypes
 import os
 

@@ -414,13 +414,13 @@ def test_store_refuses_bad_scale(backend):
 
 
 # ---------------------------------------------------------------- fast mode (tolerance-bound)
-FAST_TOL = {Q8: 1e-5, Q4: 1e-5, Q4K: 1e-4, Q6K: 1e-4}  # north star: 1e-5, 1e-4 for K-quants
+FAST_TOL = {Q8: 1e-5, Q4: 1e-5, Q4K: 1e-4, Q6K: 1e-4}  # fast-mode bound: 1e-5, 1e-4 for K-quants
 
 
 @pytest.mark.parametrize("dt", DTS)
 @pytest.mark.parametrize("N,K", [(7, 256), (64, 512), (130, 2048), (33, 4096), (200, 14336), (1024, 4096)])
 def test_gemv_fast_tolerance(backend, dt, N, K):
-    """MODE_FAST: |gpu - oracle| / (1 + |oracle|) within the north-star bound, for accumulate and set,
+    """MODE_FAST: |gpu - oracle| / (1 + |oracle|) within the fast-mode bound, for accumulate and set,
     on encoded N(0, 0.02) weights with 1% outliers and on x1000 activations."""
     raw = synth.quant_weights(dt, N, K, seed=N + K, outliers=0.01)
     w = backend.FromQuantized(dt, raw, N, K)
@@ -870,7 +870,7 @@ Q84_SHAPES = [(4096, 4096), (14336, 4096), (4096, 14336), (300, 1024), (77, 8192
 @pytest.mark.parametrize("dt", [Q8, Q4, Q6K])
 @pytest.mark.parametrize("N,K", Q84_SHAPES)
 def test_gemv_fast_q8_q4(backend, dt, N, K):
-    """Fast q8_0 / q4_0 / q6_k GEMV (K across lanes over fixed-point x) on the configs' shapes and ragged ones,
+    """Fast q8_0 / q4_0 / q6_k GEMV (K across lanes over fixed-point x) on the Llama-3-8B shapes and ragged ones,
     set and accumulate, x1 and x1000: within the 1e-5 (q8_0, q4_0) and 1e-4 (q6_k) bounds."""
     raw = synth.quant_weights(dt, N, K, seed=N + 3 * K, outliers=0.01 if dt == Q6K else 0.0)
     w = backend.FromQuantized(dt, raw, N, K)
