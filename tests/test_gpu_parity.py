@@ -710,7 +710,7 @@ def test_gemm_q_swiglu_fused_fast(backend, I, K):
 
 
 @pytest.mark.parametrize("dt", DTS)
-@pytest.mark.parametrize("M", [1, 16])
+@pytest.mark.parametrize("M", [1, 3, 16])
 @pytest.mark.parametrize("N,K", [(300, 1024), (6144, 4096), (700, 14336), (10240, 2048)])
 def test_fast_random_scale_blocks(backend, dt, M, N, K):
     """Every fast kernel (the M = 1 GEMVs, both q4_k layouts, and the M > 1 matrix-core paths) on TR's random
