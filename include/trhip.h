@@ -68,8 +68,15 @@ int trhip_alloc(trhip_ctx *ctx, size_t bytes, void **dptr);
 int trhip_free(trhip_ctx *ctx, void *dptr);
 int trhip_h2d_async(trhip_ctx *ctx, void *dst, const void *src, size_t bytes);
 int trhip_d2h(trhip_ctx *ctx, void *dst, const void *src, size_t bytes); /* waits */
+/* A fill kernel (not a memset node), so it may be captured into a graph like the compute calls. */
 int trhip_memset_async(trhip_ctx *ctx, void *dst, int value, size_t bytes);
+/* trhip_d2h, trhip_sync and trhip_free wait for the stream and fail with TRHIP_ERR_INVALID while it is captured. */
 int trhip_sync(trhip_ctx *ctx);
+
+/* Page-locked host memory (the off-heap HostBlock of tensor/host_block.go:150-200 can live here):
+ * trhip_wstore_create uploads a source inside such a block by DMA from where it is, with no staging copy. */
+int trhip_host_alloc(trhip_ctx *ctx, size_t bytes, void **hptr);
+int trhip_host_free(trhip_ctx *ctx, void *hptr);
 
 /* Stream-ordered timing events (the reference's TR_GPU_PROFILE events, gpu/profile.go:1-34). */
 int trhip_event_create(trhip_ctx *ctx, void **ev);
@@ -80,8 +87,12 @@ int trhip_event_destroy(void *ev);
 /* Stream capture into a replayable HIP graph (launch-bound sequences such as a decode sweep).
  * Every call made on ctx between begin and end is recorded, not run; trhip_graph_launch replays it
  * on the context's stream. Calls that would grow the context's workspace fail during capture: make
- * one eager call of the same shapes first. Counterpart of the reference's CUDA-graph replay
- * (gpu/graph.go); nothing on this path requires it. */
+ * one eager call of the same shapes first. A graph's nodes address the workspace as it was at
+ * capture; when a later eager call grows it, the old buffers stay allocated until the context's last
+ * graph is destroyed, so replays stay valid. Calls that wait for the stream, allocate or free
+ * (trhip_sync, trhip_d2h, trhip_free, store creation and release, host-index embedding) refuse while
+ * capturing. Counterpart of the reference's CUDA-graph replay (gpu/graph.go); nothing on this path
+ * requires it. */
 int trhip_graph_begin(trhip_ctx *ctx);
 int trhip_graph_end(trhip_ctx *ctx, void **exec);
 int trhip_graph_launch(trhip_ctx *ctx, void *exec);
@@ -92,12 +103,18 @@ int trhip_graph_destroy(void *exec);
 int trhip_check_quant_scales(int dtype, const void *raw, size_t raw_bytes, int64_t *bad_block);
 
 /* Device-resident weight store. Replaces RawBackend.FromRaw for quantized dtypes
- * (tensor/typed.go:22-30, gpu/typed.go:24-35, tensor/quant.go:75-81): raw holds N*K/blk
- * GGUF blocks in file order; they are uploaded asynchronously and repacked on the device
- * into per-field planes (codes, scales) for 128-bit coalesced loads. No value is decoded.
- * The host buffer must stay valid until the next trhip_sync on ctx. */
+ * (tensor/typed.go:22-30, gpu/typed.go:24-35, tensor/quant.go:75-81) and the load path
+ * FromHostBlock -> FromQuantized (tensor/host_block.go:180-186, stdlib/ml/load_gguf.go:79-107):
+ * raw holds N*K/blk GGUF blocks in file order. They are uploaded in chunks through pinned
+ * staging (a source inside a trhip_host_alloc block is sent by DMA directly) and repacked on
+ * the device into per-field planes (codes, scales) for 128-bit coalesced loads. No value is
+ * decoded. A pageable source is copied before the call returns; a pinned one must stay valid
+ * until the next trhip_sync on ctx. */
 int trhip_wstore_create(trhip_ctx *ctx, int dtype, const void *raw, size_t raw_bytes, int64_t N,
                         int64_t K, trhip_wstore **out);
+/* Zeroed quantized storage, tensor/quant.go:408-427 (newQuantStorage / QuantZeroRaw): every block
+ * byte 0 except the q4 codes, 0x88, so that every element opens to +0. */
+int trhip_wstore_create_zero(trhip_ctx *ctx, int dtype, int64_t N, int64_t K, trhip_wstore **out);
 int trhip_wstore_destroy(trhip_wstore *w); /* Releaser.Release, tensor/device.go:520-522 */
 int trhip_wstore_info(const trhip_wstore *w, int *dtype, int64_t *N, int64_t *K, size_t *device_bytes);
 /* One store holding the rows of several (same dtype and K), in order: the merged layers of
@@ -141,7 +158,8 @@ int trhip_open_q(trhip_ctx *ctx, const trhip_wstore *w, int64_t elem_off, int64_
 /* Backend.Embedding for a quantized table (tensor/device.go:482, tensor/cpu_quant.go:163-171):
  * out[i, :] = deq(w)[idx[i], :]; idx is a host array of nidx int64 row indices (the reference passes
  * a Go []int). Indices are checked on the host before upload; an out-of-range index returns
- * TRHIP_ERR_INVALID (H3043). The call waits until the indices are on the device. */
+ * TRHIP_ERR_INVALID (H3043). The indices are copied to pinned staging and uploaded asynchronously;
+ * the caller's array may be reused on return. Refused while the stream is captured. */
 int trhip_embedding_q(trhip_ctx *ctx, const trhip_wstore *w, const int64_t *idx, int64_t nidx, float *out);
 
 /* SwiGLU gate (lib/layers.tr:223 swiglu_gate on the [gate | up] halves of a merged gate_up output,
@@ -167,6 +185,23 @@ int trhip_quantize_q8(trhip_ctx *ctx, const float *x, int64_t M, int64_t K, int 
  * bytes 16-byte aligned) and writes nothing. One launch over a buffer that is not in the caches times
  * the device's single-launch streaming-read ceiling, the floor the GEMV kernels are measured against. */
 int trhip_read_probe(trhip_ctx *ctx, const void *p, int64_t bytes);
+
+/* Diagnostic with no counterpart in the reference: one workgroup per CU of 4 * waves_per_simd waves, each running
+ * iters rounds of four independent v_mfma_i32_32x32x32_i8 (262,144 int8 ops per round) with valu_per_mfma
+ * (0, 2, 4, 6, 8, 12 or 16) independent fp32 FMAs issued beside each MFMA. Timed with events it gives the device's
+ * int8 matrix-core rate and how much VALU work hides under it, the ceiling of the prefill kernel. */
+int trhip_mfma_probe(trhip_ctx *ctx, int valu_per_mfma, int waves_per_simd, int64_t iters);
+
+/* Test and tuning hook with no counterpart in the reference: force a launch shape on this context
+ * instead of the built-in choice (all four values 0 restores it). Shapes that are not built are
+ * refused here, never at a later GEMV. TRHIP_KNOB_KL: K-across-lanes fast GEMV (a, b, c, d) =
+ * (waves, K parts, rows in flight, rows per wave); TRHIP_KNOB_FAST_Q4K: row-sliced fast q4_k GEMV
+ * (blocks in flight, waves, K parts, rows per lane); TRHIP_KNOB_EXACT_ROWS: exact four-lane GEMV rows
+ * per workgroup a; TRHIP_KNOB_EXACT_LANES: exact GEMV lanes per row a; TRHIP_KNOB_ACTQ_TM: act-quant
+ * MFMA row tile a. */
+enum { TRHIP_KNOB_KL = 1, TRHIP_KNOB_FAST_Q4K = 2, TRHIP_KNOB_EXACT_ROWS = 3, TRHIP_KNOB_EXACT_LANES = 4,
+       TRHIP_KNOB_ACTQ_TM = 5 };
+int trhip_set_launch_shape(trhip_ctx *ctx, int knob, int a, int b, int c, int d);
 
 #ifdef __cplusplus
 }

@@ -29,6 +29,8 @@ SIGNATURES = [
     ("trhip_d2h", INT, [P, P, P, SZ]),
     ("trhip_memset_async", INT, [P, P, INT, SZ]),
     ("trhip_sync", INT, [P]),
+    ("trhip_host_alloc", INT, [P, SZ, ctypes.POINTER(P)]),
+    ("trhip_host_free", INT, [P, P]),
     ("trhip_event_create", INT, [P, ctypes.POINTER(P)]),
     ("trhip_event_record", INT, [P, P]),
     ("trhip_event_elapsed_ms", INT, [P, P, ctypes.POINTER(ctypes.c_float)]),
@@ -39,6 +41,7 @@ SIGNATURES = [
     ("trhip_graph_destroy", INT, [P]),
     ("trhip_check_quant_scales", INT, [INT, P, SZ, ctypes.POINTER(I64)]),
     ("trhip_wstore_create", INT, [P, INT, P, SZ, I64, I64, ctypes.POINTER(P)]),
+    ("trhip_wstore_create_zero", INT, [P, INT, I64, I64, ctypes.POINTER(P)]),
     ("trhip_wstore_destroy", INT, [P]),
     ("trhip_wstore_info", INT, [P, ctypes.POINTER(INT), ctypes.POINTER(I64), ctypes.POINTER(I64), ctypes.POINTER(SZ)]),
     ("trhip_wstore_to_raw", INT, [P, P, I64, I64, P]),
@@ -47,16 +50,19 @@ SIGNATURES = [
     ("trhip_gemm_q_actq", INT, [P, P, I64, I64, P, P, I64, I64, INT]),
     ("trhip_open_q", INT, [P, P, I64, I64, P]),
     ("trhip_read_probe", INT, [P, P, I64]),
+    ("trhip_mfma_probe", INT, [P, INT, INT, I64]),
     ("trhip_embedding_q", INT, [P, P, P, I64, P]),
     ("trhip_quantize_q8", INT, [P, P, I64, I64, INT, P, P, P]),
     ("trhip_swiglu", INT, [P, P, I64, I64, P]),
     ("trhip_gemm_q_swiglu", INT, [P, P, P, P, I64, I64, INT]),
+    ("trhip_set_launch_shape", INT, [P, INT, INT, INT, INT, INT]),
 ]
 
 # Status codes and enums (include/trhip.h)
 OK, ERR_INVALID, ERR_OOM, ERR_HIP, ERR_LAUNCH, ERR_UNSUPPORTED, ERR_NO_DEVICE, ERR_BAD_SCALE = range(8)
 Q8, Q4, Q4K, Q6K = 1, 2, 3, 4
 MODE_EXACT, MODE_FAST = 0, 1
+KNOB_KL, KNOB_FAST_Q4K, KNOB_EXACT_ROWS, KNOB_EXACT_LANES, KNOB_ACTQ_TM = 1, 2, 3, 4, 5
 
 
 def load(path=LIB_PATH):

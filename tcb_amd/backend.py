@@ -9,6 +9,7 @@ Names and argument meaning follow the reference's Backend slice for this path
   QuantBackend.GemmActQuant(M, N, K, a, w, c)    ActQuantGemmer.GemmActQuant, matmul.go:59-61
   QuantBackend.OpenQuant(out, w, offset, n)      QuantOpener.OpenQuant, quant.go:103-105
   QuantBackend.Embedding(out, w, idx)            Backend.Embedding, device.go:482
+  QuantBackend.NewQuantStorage(dt, N, K)        newQuantStorage / QuantZeroRaw, quant.go:408-427
   QuantWeight.ToRaw(row0, rows)                  RawBackend.ToRaw, typed.go:27
   CheckQuantScales(dt, raw)                      tensor/quant.go:108-128
 
@@ -120,6 +121,20 @@ class Context:
     def record(self, ev):
         _check(_lib.lib().trhip_event_record(self.h, ev), self.h)
 
+    def host_alloc(self, nbytes):
+        """Page-locked host memory as a numpy uint8 array (trhip_host_alloc); free with host_free."""
+        p = P()
+        _check(_lib.lib().trhip_host_alloc(self.h, max(int(nbytes), 1), ctypes.byref(p)), self.h)
+        arr = np.ctypeslib.as_array((ctypes.c_uint8 * max(int(nbytes), 1)).from_address(p.value))[:int(nbytes)]
+        return arr, p
+
+    def host_free(self, p):
+        _check(_lib.lib().trhip_host_free(self.h, p), self.h)
+
+    def set_launch_shape(self, knob, a=0, b=0, c=0, d=0):
+        """Force a launch shape (tests and tuning; all zero restores the built-in choice)."""
+        _check(_lib.lib().trhip_set_launch_shape(self.h, knob, a, b, c, d), self.h)
+
     def read_probe(self, buf, nbytes=None):
         """Read nbytes of buf once on the device (the single-launch streaming-read ceiling; writes nothing)."""
         _check(_lib.lib().trhip_read_probe(self.h, buf.addr(), buf.nbytes if nbytes is None else nbytes), self.h)
@@ -139,12 +154,14 @@ class Context:
 class QuantWeight:
     """Device-resident GGUF weight [N, K] (trhip_wstore)."""
 
-    def __init__(self, ctx, dt, raw, N, K):
+    def __init__(self, ctx, dt, raw, N, K, zero=False):
         self.ctx = ctx
         self.dt = dtype_code(dt)
         self.N, self.K = int(N), int(K)
-        if raw is None:  # filled by the caller (Concat)
+        if raw is None:  # filled by the caller (Concat) or zeroed
             self.h = P()
+            if zero:
+                _check(_lib.lib().trhip_wstore_create_zero(ctx.h, self.dt, self.N, self.K, ctypes.byref(self.h)), ctx.h)
             return
         raw = np.ascontiguousarray(raw, dtype=np.uint8)
         h = P()
@@ -195,6 +212,10 @@ class QuantBackend:
 
     def FromQuantized(self, dt, raw, N, K):
         return QuantWeight(self.ctx, dt, raw, N, K)
+
+    def NewQuantStorage(self, dt, N, K):
+        """Zeroed quantized storage: every element opens to +0 (tensor/quant.go:408-427)."""
+        return QuantWeight(self.ctx, dt, None, N, K, zero=True)
 
     def Gemm(self, M, N, K, a, w, c, row0=0, mode=MODE_EXACT):
         _check(_lib.lib().trhip_gemm_q(self.ctx.h, w.h, row0, N, _ptr(a), _ptr(c), M, K, 1, mode), self.ctx.h)

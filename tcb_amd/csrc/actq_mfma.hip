@@ -269,16 +269,7 @@ int run_mfma(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, con
              bool acc, const int8_t *q, const float *d, const uint16_t *sj, const uint8_t *bad) {
     constexpr size_t lds = Tile<TM>::LDS;
     dim3 grid((unsigned)(((N + TN - 1) / TN) * ((M + TM - 1) / TM))), block(THREADS);
-    static bool lds_set = false;  // more than 64 KB of dynamic LDS has to be allowed once per kernel
-    if (!lds_set) {
-        hipError_t e1 = hipFuncSetAttribute(reinterpret_cast<const void *>(&actq_mfma_q4k<true, TM>),
-                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        hipError_t e2 = hipFuncSetAttribute(reinterpret_cast<const void *>(&actq_mfma_q4k<false, TM>),
-                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e1 != hipSuccess) return hip_fail(ctx, e1, "actq_mfma: LDS size");
-        if (e2 != hipSuccess) return hip_fail(ctx, e2, "actq_mfma: LDS size");
-        lds_set = true;
-    }
+    static_assert(lds <= 64 * 1024, "below 64 KB of LDS no launch attribute is needed");
     if (acc)
         hipLaunchKernelGGL((actq_mfma_q4k<true, TM>), grid, block, lds, ctx->stream, w->planes(), N, row0, M, w->K, x, q, d,
                            sj, bad, c);
@@ -1058,13 +1049,9 @@ int launch_actq_mfma(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_
     if (w->dtype != kQ4K) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "actq_mfma: q4_k only");
     // Row-tile height: 64 rows unless that leaves fewer than 160 workgroups (measured: 4096 x 14336 at M = 128
     // takes 74 us on 32-row tiles against 104 on 64; 14336 x 4096 at M = 128 or 512 is faster on 64).
-    // TRHIP_ACTQ_TM (32 or 64) overrides.
-    static const int tm_env = [] {
-        const char *e = getenv("TRHIP_ACTQ_TM");
-        return e ? atoi(e) : 0;
-    }();
+    // trhip_set_launch_shape(TRHIP_KNOB_ACTQ_TM) overrides.
     const int64_t wgs64 = ((N + TN - 1) / TN) * ((M + 63) / 64);
-    const int tm = tm_env == 32 || tm_env == 64 ? tm_env : (wgs64 < 160 ? 32 : 64);
+    const int tm = ctx->force_actq_tm ? ctx->force_actq_tm : (wgs64 < 160 ? 32 : 64);
     if (tm == 32) return run_mfma<32>(ctx, w, row0, N, x, c, M, acc, q, d, sj, bad);
     return run_mfma<64>(ctx, w, row0, N, x, c, M, acc, q, d, sj, bad);
 }

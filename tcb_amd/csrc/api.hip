@@ -9,6 +9,7 @@
 #include <cstdio>
 #include <cstring>
 #include <new>
+#include <thread>
 #include <vector>
 
 namespace trhip {
@@ -29,45 +30,54 @@ int launch_check(trhip_ctx *ctx, const char *what) {
     return TRHIP_OK;
 }
 
-void *workspace(trhip_ctx *ctx, size_t bytes, int *status) {
-    *status = TRHIP_OK;
-    if (bytes <= ctx->ws_bytes) return ctx->ws;
+bool capturing(trhip_ctx *ctx) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(ctx->stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
+    return hipStreamIsCapturing(ctx->stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
+namespace {
+// Grow one of the context's workspace buffers to at least `bytes`. The old buffer is freed at once when no
+// instantiated graph of this context exists, else kept on the retired list (a graph's nodes may hold its address).
+void *grow(trhip_ctx *ctx, void *&buf, size_t &have, size_t bytes, int *status) {
+    *status = TRHIP_OK;
+    if (bytes <= have) return buf;
+    if (capturing(ctx)) {
         *status = fail(ctx, TRHIP_ERR_INVALID, "workspace must be sized by an eager call before graph capture");
         return nullptr;
     }
     // Growing: earlier work on the stream may still read the old buffer.
     hipError_t e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) { *status = hip_fail(ctx, e, "workspace sync"); return nullptr; }
-    if (ctx->ws) (void)hipFree(ctx->ws);
-    ctx->ws = nullptr;
-    ctx->ws_bytes = 0;
+    if (buf) {
+        if (ctx->live_graphs > 0) ctx->retired.push_back(buf);
+        else (void)hipFree(buf);
+    }
+    buf = nullptr;
+    have = 0;
     size_t want = bytes < (size_t)(1 << 20) ? (size_t)(1 << 20) : bytes + bytes / 4;
-    e = hipMalloc(&ctx->ws, want);
-    if (e != hipSuccess) { ctx->ws = nullptr; *status = hip_fail(ctx, e, "workspace alloc"); return nullptr; }
-    ctx->ws_bytes = want;
-    return ctx->ws;
+    e = hipMalloc(&buf, want);
+    if (e != hipSuccess) { buf = nullptr; *status = hip_fail(ctx, e, "workspace alloc"); return nullptr; }
+    have = want;
+    return buf;
 }
+}  // namespace
+
+void *workspace(trhip_ctx *ctx, size_t bytes, int *status) { return grow(ctx, ctx->ws, ctx->ws_bytes, bytes, status); }
 
 void *workspace2(trhip_ctx *ctx, size_t bytes, int *status) {
-    *status = TRHIP_OK;
-    if (bytes <= ctx->ws2_bytes) return ctx->ws2;
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(ctx->stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
-        *status = fail(ctx, TRHIP_ERR_INVALID, "workspace must be sized by an eager call before graph capture");
-        return nullptr;
-    }
-    hipError_t e = hipStreamSynchronize(ctx->stream);
-    if (e != hipSuccess) { *status = hip_fail(ctx, e, "workspace sync"); return nullptr; }
-    if (ctx->ws2) (void)hipFree(ctx->ws2);
-    ctx->ws2 = nullptr;
-    ctx->ws2_bytes = 0;
-    size_t want = bytes < (size_t)(1 << 20) ? (size_t)(1 << 20) : bytes + bytes / 4;
-    e = hipMalloc(&ctx->ws2, want);
-    if (e != hipSuccess) { ctx->ws2 = nullptr; *status = hip_fail(ctx, e, "workspace alloc"); return nullptr; }
-    ctx->ws2_bytes = want;
-    return ctx->ws2;
+    return grow(ctx, ctx->ws2, ctx->ws2_bytes, bytes, status);
+}
+
+int allow_dyn_lds(trhip_ctx *ctx, const void *fn, size_t bytes, const char *what) {
+    static std::mutex mu;
+    static std::vector<std::pair<int, const void *>> done;
+    std::lock_guard<std::mutex> lk(mu);
+    for (const auto &d : done)
+        if (d.first == ctx->device && d.second == fn) return TRHIP_OK;
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (e != hipSuccess) return hip_fail(ctx, e, what);
+    done.emplace_back(ctx->device, fn);
+    return TRHIP_OK;
 }
 
 __global__ void zero_f32_kernel(float *__restrict__ p, int64_t n) {
@@ -80,6 +90,32 @@ int zero_f32(trhip_ctx *ctx, float *p, int64_t n) {
     if (n <= 0) return TRHIP_OK;
     hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream, p, n);
     return launch_check(ctx, "zero");
+}
+
+// Byte fill: thread i writes bytes [16 i, 16 i + 16) of the range, one 16-byte store where the range is 16-byte
+// aligned there, else byte stores.
+__global__ void fill_bytes_kernel(uint8_t *__restrict__ p, uint32_t word, int64_t bytes) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x, o = 16 * i;
+    if (o >= bytes) return;
+    uint8_t *q = p + o;
+    if (o + 16 <= bytes && reinterpret_cast<uintptr_t>(q) % 16 == 0) {
+        *reinterpret_cast<uint4 *>(q) = make_uint4(word, word, word, word);
+    } else {
+        const int64_t n = bytes - o < 16 ? bytes - o : 16;
+        for (int64_t k = 0; k < n; k++) q[k] = (uint8_t)word;
+    }
+}
+
+// Fill bytes with a value by a kernel (a memset node in a captured graph has given wrong results on replays).
+int fill_bytes(trhip_ctx *ctx, void *p, int value, size_t bytes) {
+    if (!bytes) return TRHIP_OK;
+    const int64_t units = ((int64_t)bytes + 15) / 16;
+    const int64_t blocks = (units + 255) / 256;
+    if (blocks >= ((int64_t)1 << 31)) return fail(ctx, TRHIP_ERR_INVALID, "memset: too large");
+    const uint32_t b = (uint32_t)(value & 0xFF), word = b | (b << 8) | (b << 16) | (b << 24);
+    hipLaunchKernelGGL(fill_bytes_kernel, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, static_cast<uint8_t *>(p),
+                       word, (int64_t)bytes);
+    return launch_check(ctx, "memset");
 }
 
 }  // namespace trhip
@@ -172,6 +208,14 @@ int trhip_destroy(trhip_ctx *ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->ws) (void)hipFree(ctx->ws);
     if (ctx->ws2) (void)hipFree(ctx->ws2);
+    for (void *p : ctx->retired) (void)hipFree(p);
+    if (ctx->idx_host) (void)hipHostFree(ctx->idx_host);
+    if (ctx->idx_done) (void)hipEventDestroy(ctx->idx_done);
+    for (int s = 0; s < trhip_ctx::UP_SLOTS; s++) {
+        if (ctx->up_host[s]) (void)hipHostFree(ctx->up_host[s]);
+        if (ctx->up_dev[s]) (void)hipFree(ctx->up_dev[s]);
+        if (ctx->up_done[s]) (void)hipEventDestroy(ctx->up_done[s]);
+    }
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return TRHIP_OK;
@@ -192,6 +236,7 @@ int trhip_free(trhip_ctx *ctx, void *dptr) {
     if (!ctx) return TRHIP_ERR_INVALID;
     DevGuard g(ctx);
     if (!dptr) return TRHIP_OK;
+    if (capturing(ctx)) return fail(ctx, TRHIP_ERR_INVALID, "free: not allowed while the stream is captured");
     hipError_t e = hipStreamSynchronize(ctx->stream);
     if (e == hipSuccess) e = hipFree(dptr);
     return e == hipSuccess ? TRHIP_OK : hip_fail(ctx, e, "free");
@@ -208,6 +253,7 @@ int trhip_h2d_async(trhip_ctx *ctx, void *dst, const void *src, size_t bytes) {
 int trhip_d2h(trhip_ctx *ctx, void *dst, const void *src, size_t bytes) {
     if (!ctx || (bytes && (!dst || !src))) return TRHIP_ERR_INVALID;
     DevGuard g(ctx);
+    if (capturing(ctx)) return fail(ctx, TRHIP_ERR_INVALID, "d2h: waits for the stream; not allowed while it is captured");
     hipError_t e = bytes ? hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream) : hipSuccess;
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     return e == hipSuccess ? TRHIP_OK : hip_fail(ctx, e, "d2h");
@@ -217,13 +263,13 @@ int trhip_memset_async(trhip_ctx *ctx, void *dst, int value, size_t bytes) {
     if (!ctx || (bytes && !dst)) return TRHIP_ERR_INVALID;
     if (!bytes) return TRHIP_OK;
     DevGuard g(ctx);
-    hipError_t e = hipMemsetAsync(dst, value, bytes, ctx->stream);
-    return e == hipSuccess ? TRHIP_OK : hip_fail(ctx, e, "memset");
+    return fill_bytes(ctx, dst, value, bytes);  // a kernel, so that it can be captured like every other call
 }
 
 int trhip_sync(trhip_ctx *ctx) {
     if (!ctx) return TRHIP_ERR_INVALID;
     DevGuard g(ctx);
+    if (capturing(ctx)) return fail(ctx, TRHIP_ERR_INVALID, "sync: not allowed while the stream is captured");
     hipError_t e = hipStreamSynchronize(ctx->stream);
     return e == hipSuccess ? TRHIP_OK : hip_fail(ctx, e, "sync");
 }
@@ -264,6 +310,16 @@ int trhip_graph_begin(trhip_ctx *ctx) {
     return e == hipSuccess ? TRHIP_OK : hip_fail(ctx, e, "graph begin");
 }
 
+}  // extern "C"
+
+// The opaque graph handle: the instantiated graph and the context whose workspace its nodes may address.
+struct trhip_graph {
+    hipGraphExec_t exec = nullptr;
+    trhip_ctx *ctx = nullptr;
+};
+
+extern "C" {
+
 int trhip_graph_end(trhip_ctx *ctx, void **exec) {
     if (!ctx || !exec) return TRHIP_ERR_INVALID;
     DevGuard g(ctx);
@@ -271,24 +327,88 @@ int trhip_graph_end(trhip_ctx *ctx, void **exec) {
     hipGraph_t graph = nullptr;
     hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
     if (e != hipSuccess) return hip_fail(ctx, e, "graph end");
-    hipGraphExec_t ge = nullptr;
-    e = hipGraphInstantiate(&ge, graph, nullptr, nullptr, 0);
-    (void)hipGraphDestroy(graph);
-    if (e != hipSuccess) return hip_fail(ctx, e, "graph instantiate");
-    *exec = (void *)ge;
+    trhip_graph *tg = new (std::nothrow) trhip_graph();
+    if (!tg) {
+        (void)hipGraphDestroy(graph);
+        return fail(ctx, TRHIP_ERR_OOM, "graph end: host allocation");
+    }
+    e = hipGraphInstantiate(&tg->exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);  // the executable graph keeps its own copy of the nodes
+    if (e != hipSuccess) {
+        delete tg;
+        return hip_fail(ctx, e, "graph instantiate");
+    }
+    tg->ctx = ctx;
+    ctx->live_graphs++;
+    *exec = (void *)tg;
     return TRHIP_OK;
 }
 
 int trhip_graph_launch(trhip_ctx *ctx, void *exec) {
     if (!ctx || !exec) return TRHIP_ERR_INVALID;
+    trhip_graph *tg = static_cast<trhip_graph *>(exec);
+    if (tg->ctx != ctx) return fail(ctx, TRHIP_ERR_INVALID, "graph launch: graph of another context");
     DevGuard g(ctx);
-    hipError_t e = hipGraphLaunch((hipGraphExec_t)exec, ctx->stream);
+    hipError_t e = hipGraphLaunch(tg->exec, ctx->stream);
     return e == hipSuccess ? TRHIP_OK : hip_fail(ctx, e, "graph launch");
 }
 
 int trhip_graph_destroy(void *exec) {
     if (!exec) return TRHIP_ERR_INVALID;
-    return hipGraphExecDestroy((hipGraphExec_t)exec) == hipSuccess ? TRHIP_OK : TRHIP_ERR_HIP;
+    trhip_graph *tg = static_cast<trhip_graph *>(exec);
+    trhip_ctx *ctx = tg->ctx;
+    DevGuard g(ctx);
+    // a replay may still be running on the stream
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    hipError_t e2 = hipGraphExecDestroy(tg->exec);
+    delete tg;
+    if (--ctx->live_graphs == 0) {  // no node can address a retired workspace buffer any more
+        for (void *p : ctx->retired) (void)hipFree(p);
+        ctx->retired.clear();
+    }
+    if (e != hipSuccess) return hip_fail(ctx, e, "graph destroy: sync");
+    return e2 == hipSuccess ? TRHIP_OK : hip_fail(ctx, e2, "graph destroy");
+}
+
+int trhip_set_launch_shape(trhip_ctx *ctx, int knob, int a, int b, int c, int d) {
+    if (!ctx) return TRHIP_ERR_INVALID;
+    const bool reset = a == 0 && b == 0 && c == 0 && d == 0;
+    switch (knob) {
+    case TRHIP_KNOB_KL: {  // WAVES, KS, PD, RPW: the instantiated K-across-lanes shapes
+        const int code = 1000 * a + 100 * b + 10 * c + d / 8;
+        static const int ok[] = {4141, 4142, 4122, 8141, 4242, 4241, 8241, 8441};
+        bool found = reset;
+        for (int v : ok) found = found || (v == code && d % 8 == 0);
+        if (!found) return fail(ctx, TRHIP_ERR_INVALID, "set_launch_shape: no such K-across-lanes shape");
+        ctx->force_kl = reset ? 0 : code;
+        return TRHIP_OK;
+    }
+    case TRHIP_KNOB_FAST_Q4K: {  // D, WAVES, KS, R of the row-sliced q4_k kernel
+        const int code = 1000 * a + 100 * b + 10 * c + d;
+        static const int ok[] = {2441, 2841, 2421, 2411, 2422, 8421};
+        bool found = reset;
+        for (int v : ok) found = found || v == code;
+        if (!found) return fail(ctx, TRHIP_ERR_INVALID, "set_launch_shape: no such row-sliced q4_k shape");
+        ctx->force_fast_q4k = reset ? 0 : code;
+        return TRHIP_OK;
+    }
+    case TRHIP_KNOB_EXACT_ROWS:
+        if (!(reset || ((a == 16 || a == 32 || a == 64) && !b && !c && !d)))
+            return fail(ctx, TRHIP_ERR_INVALID, "set_launch_shape: exact rows per workgroup must be 16, 32 or 64");
+        ctx->force_exact_rows = a;
+        return TRHIP_OK;
+    case TRHIP_KNOB_EXACT_LANES:
+        if (!(reset || ((a == 4 || a == 8) && !b && !c && !d)))
+            return fail(ctx, TRHIP_ERR_INVALID, "set_launch_shape: exact lanes per row must be 4 or 8");
+        ctx->force_exact_lanes = a;
+        return TRHIP_OK;
+    case TRHIP_KNOB_ACTQ_TM:
+        if (!(reset || ((a == 32 || a == 64) && !b && !c && !d)))
+            return fail(ctx, TRHIP_ERR_INVALID, "set_launch_shape: act-quant row tile must be 32 or 64");
+        ctx->force_actq_tm = a;
+        return TRHIP_OK;
+    }
+    return fail(ctx, TRHIP_ERR_INVALID, "set_launch_shape: unknown knob");
 }
 
 int trhip_check_quant_scales(int dtype, const void *raw, size_t raw_bytes, int64_t *bad_block) {
@@ -311,31 +431,21 @@ int trhip_check_quant_scales(int dtype, const void *raw, size_t raw_bytes, int64
     return TRHIP_OK;
 }
 
-int trhip_wstore_create(trhip_ctx *ctx, int dtype, const void *raw, size_t raw_bytes, int64_t N, int64_t K,
-                        trhip_wstore **out) {
-    if (!ctx || !out) return TRHIP_ERR_INVALID;
-    *out = nullptr;
-    if (bad_dtype(dtype)) return fail(ctx, TRHIP_ERR_INVALID, "wstore: unknown dtype");
-    if (N < 0 || K < 0 || K % block_elems(dtype) != 0)  // H6692: last axis must be a multiple of the block
-        return fail(ctx, TRHIP_ERR_INVALID, "wstore: K must be a non-negative multiple of the block size");
-    int64_t nb = K / block_elems(dtype);
-    size_t need = (size_t)(N * nb) * (size_t)block_bytes(dtype);
-    if (raw_bytes != need || (need && !raw))  // H3035
-        return fail(ctx, TRHIP_ERR_INVALID, "wstore: raw size does not match N*K");
-    int64_t bad = -1;
-    trhip_check_quant_scales(dtype, raw, raw_bytes, &bad);
-    if (bad >= 0) return fail(ctx, TRHIP_ERR_BAD_SCALE, "wstore: block " + std::to_string(bad) + " has a NaN/Inf scale (H6686)");
-    DevGuard g(ctx);
+}  // extern "C"
+
+namespace {
+
+// Planes of a new store of N x K (one allocation; layout in trhip_internal.hpp).
+int new_store(trhip_ctx *ctx, int dtype, int64_t N, int64_t K, trhip_wstore **out) {
     trhip_wstore *w = new (std::nothrow) trhip_wstore();
-    if (!w) return TRHIP_ERR_OOM;
+    if (!w) return fail(ctx, TRHIP_ERR_OOM, "wstore: host allocation");
     w->ctx = ctx;
     w->dtype = dtype;
     w->N = N;
     w->K = K;
-    w->nb = nb;
-    size_t nblk = (size_t)(N * nb);
-    size_t o_qs = 0;
-    size_t o_aux = align_up(o_qs + nblk * qs_bytes(dtype), 256);
+    w->nb = K / block_elems(dtype);
+    size_t nblk = (size_t)(N * w->nb);
+    size_t o_aux = align_up(nblk * qs_bytes(dtype), 256);
     size_t o_sc = align_up(o_aux + nblk * aux_bytes(dtype), 256);
     size_t o_d = align_up(o_sc + nblk * sc_bytes(dtype), 256);
     size_t total = align_up(o_d + nblk * d_bytes(dtype), 256);
@@ -345,22 +455,183 @@ int trhip_wstore_create(trhip_ctx *ctx, int dtype, const void *raw, size_t raw_b
         return hip_fail(ctx, e, "wstore alloc");
     }
     w->bytes = total;
-    w->qs = w->base + o_qs;
+    w->qs = w->base;
     w->aux = aux_bytes(dtype) ? w->base + o_aux : nullptr;
     w->sc = sc_bytes(dtype) ? w->base + o_sc : nullptr;
     w->d = d_bytes(dtype) ? reinterpret_cast<uint16_t *>(w->base + o_d) : nullptr;
-    if (need) {
-        uint8_t *stage = nullptr;
-        e = hipMallocAsync((void **)&stage, need, ctx->stream);
-        if (e == hipSuccess) e = hipMemcpyAsync(stage, raw, need, hipMemcpyHostToDevice, ctx->stream);
-        int st = e == hipSuccess ? launch_repack(ctx, w, stage) : hip_fail(ctx, e, "wstore upload");
-        if (stage) (void)hipFreeAsync(stage, ctx->stream);
-        if (st != TRHIP_OK) {
-            (void)hipStreamSynchronize(ctx->stream);
-            (void)hipFree(w->base);
-            delete w;
-            return st;
+    *out = w;
+    return TRHIP_OK;
+}
+
+void drop_store(trhip_wstore *w) {
+    (void)hipStreamSynchronize(w->ctx->stream);
+    (void)hipFree(w->base);
+    delete w;
+}
+
+// Host allocations made by trhip_host_alloc (pinned, page-locked): uploads from inside one need no staging copy.
+std::mutex g_pinned_mu;
+std::vector<std::pair<uintptr_t, size_t>> g_pinned;
+
+bool inside_pinned(const void *p, size_t bytes) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    std::lock_guard<std::mutex> lk(g_pinned_mu);
+    for (const auto &r : g_pinned)
+        if (a >= r.first && a + bytes <= r.first + r.second) return true;
+    return false;
+}
+
+constexpr size_t kUpSlot = (size_t)32 << 20;  // bytes per slot of the upload ring
+
+// The context's upload ring: two pinned host buffers and two device staging buffers, made on first use.
+int upload_ring(trhip_ctx *ctx) {
+    if (ctx->up_slot_bytes) return TRHIP_OK;
+    hipError_t e = hipSuccess;
+    for (int s = 0; s < trhip_ctx::UP_SLOTS && e == hipSuccess; s++) {
+        e = hipHostMalloc(&ctx->up_host[s], kUpSlot, hipHostMallocDefault);
+        if (e == hipSuccess) e = hipMalloc(&ctx->up_dev[s], kUpSlot);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->up_done[s], hipEventDisableTiming);
+    }
+    if (e != hipSuccess) {
+        for (int s = 0; s < trhip_ctx::UP_SLOTS; s++) {
+            if (ctx->up_host[s]) (void)hipHostFree(ctx->up_host[s]);
+            if (ctx->up_dev[s]) (void)hipFree(ctx->up_dev[s]);
+            if (ctx->up_done[s]) (void)hipEventDestroy(ctx->up_done[s]);
+            ctx->up_host[s] = ctx->up_dev[s] = nullptr;
+            ctx->up_done[s] = nullptr;
         }
+        return hip_fail(ctx, e, "wstore: upload ring");
+    }
+    ctx->up_slot_bytes = kUpSlot;
+    return TRHIP_OK;
+}
+
+// memcpy split over a few threads (pageable source -> pinned staging); small copies stay on the calling thread.
+void par_memcpy(void *dst, const void *src, size_t n) {
+    constexpr int T = 4;
+    if (n < ((size_t)4 << 20)) {
+        std::memcpy(dst, src, n);
+        return;
+    }
+    const size_t part = (n / T + 63) / 64 * 64;
+    std::thread th[T - 1];
+    for (int t = 1; t < T; t++) {
+        const size_t o = part * t;
+        const size_t len = o >= n ? 0 : (n - o < part ? n - o : part);
+        th[t - 1] = std::thread([=] { if (len) std::memcpy(static_cast<char *>(dst) + o, static_cast<const char *>(src) + o, len); });
+    }
+    std::memcpy(dst, src, part < n ? part : n);
+    for (auto &t : th) t.join();
+}
+
+}  // namespace
+
+extern "C" {
+
+int trhip_host_alloc(trhip_ctx *ctx, size_t bytes, void **hptr) {
+    if (!ctx || !hptr) return TRHIP_ERR_INVALID;
+    DevGuard g(ctx);
+    *hptr = nullptr;
+    hipError_t e = hipHostMalloc(hptr, bytes ? bytes : 1, hipHostMallocDefault);
+    if (e != hipSuccess) {
+        *hptr = nullptr;
+        return hip_fail(ctx, e, "host alloc");
+    }
+    std::lock_guard<std::mutex> lk(g_pinned_mu);
+    g_pinned.emplace_back(reinterpret_cast<uintptr_t>(*hptr), bytes ? bytes : 1);
+    return TRHIP_OK;
+}
+
+int trhip_host_free(trhip_ctx *ctx, void *hptr) {
+    if (!ctx) return TRHIP_ERR_INVALID;
+    if (!hptr) return TRHIP_OK;
+    DevGuard g(ctx);
+    {
+        std::lock_guard<std::mutex> lk(g_pinned_mu);
+        size_t i = 0;
+        for (; i < g_pinned.size() && g_pinned[i].first != reinterpret_cast<uintptr_t>(hptr); i++) {}
+        if (i == g_pinned.size()) return fail(ctx, TRHIP_ERR_INVALID, "host free: not from trhip_host_alloc");
+        g_pinned.erase(g_pinned.begin() + (ptrdiff_t)i);
+    }
+    // a copy from it may still be queued
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e == hipSuccess) e = hipHostFree(hptr);
+    return e == hipSuccess ? TRHIP_OK : hip_fail(ctx, e, "host free");
+}
+
+int trhip_wstore_create(trhip_ctx *ctx, int dtype, const void *raw, size_t raw_bytes, int64_t N, int64_t K,
+                        trhip_wstore **out) {
+    if (!ctx || !out) return TRHIP_ERR_INVALID;
+    *out = nullptr;
+    if (bad_dtype(dtype)) return fail(ctx, TRHIP_ERR_INVALID, "wstore: unknown dtype");
+    if (N < 0 || K < 0 || K % block_elems(dtype) != 0)  // H6692: last axis must be a multiple of the block
+        return fail(ctx, TRHIP_ERR_INVALID, "wstore: K must be a non-negative multiple of the block size");
+    const int64_t nb = K / block_elems(dtype), bb = block_bytes(dtype);
+    size_t need = (size_t)(N * nb) * (size_t)bb;
+    if (raw_bytes != need || (need && !raw))  // H3035
+        return fail(ctx, TRHIP_ERR_INVALID, "wstore: raw size does not match N*K");
+    int64_t bad = -1;
+    trhip_check_quant_scales(dtype, raw, raw_bytes, &bad);
+    if (bad >= 0) return fail(ctx, TRHIP_ERR_BAD_SCALE, "wstore: block " + std::to_string(bad) + " has a NaN/Inf scale (H6686)");
+    DevGuard g(ctx);
+    if (capturing(ctx)) return fail(ctx, TRHIP_ERR_INVALID, "wstore: not allowed while the stream is captured");
+    trhip_wstore *w = nullptr;
+    int st = new_store(ctx, dtype, N, K, &w);
+    if (st != TRHIP_OK) return st;
+    if (need && (st = upload_ring(ctx)) != TRHIP_OK) {
+        drop_store(w);
+        return st;
+    }
+    // Chunks of whole blocks (a multiple of 8, so every chunk starts 16-byte aligned in each plane) go through the
+    // two-slot ring: the host copies chunk i into pinned slot i % 2 while the DMA engine uploads chunk i - 1 and the
+    // device repacks it. A source inside a trhip_host_alloc block is uploaded from where it is.
+    const bool pinned = inside_pinned(raw, need);
+    const int64_t nblk = N * nb, per = (int64_t)(kUpSlot / (size_t)bb) / 8 * 8;
+    const uint8_t *src0 = static_cast<const uint8_t *>(raw);
+    for (int64_t b0 = 0, i = 0; b0 < nblk && st == TRHIP_OK; b0 += per, i++) {
+        const int s = (int)(i % trhip_ctx::UP_SLOTS);
+        const int64_t nbk = nblk - b0 < per ? nblk - b0 : per;
+        const size_t bytes = (size_t)(nbk * bb);
+        const void *src = src0 + (size_t)(b0 * bb);
+        hipError_t e = hipSuccess;
+        if (!pinned) {
+            e = hipEventSynchronize(ctx->up_done[s]);  // the slot's previous upload has left it
+            if (e == hipSuccess) {
+                par_memcpy(ctx->up_host[s], src, bytes);
+                src = ctx->up_host[s];
+            }
+        }
+        if (e == hipSuccess) e = hipMemcpyAsync(ctx->up_dev[s], src, bytes, hipMemcpyHostToDevice, ctx->stream);
+        if (e == hipSuccess) e = hipEventRecord(ctx->up_done[s], ctx->stream);
+        st = e == hipSuccess ? launch_repack(ctx, w, static_cast<const uint8_t *>(ctx->up_dev[s]), b0, nbk)
+                             : hip_fail(ctx, e, "wstore upload");
+    }
+    if (st != TRHIP_OK) {
+        drop_store(w);
+        return st;
+    }
+    *out = w;
+    return TRHIP_OK;
+}
+
+int trhip_wstore_create_zero(trhip_ctx *ctx, int dtype, int64_t N, int64_t K, trhip_wstore **out) {
+    if (!ctx || !out) return TRHIP_ERR_INVALID;
+    *out = nullptr;
+    if (bad_dtype(dtype)) return fail(ctx, TRHIP_ERR_INVALID, "wstore_zero: unknown dtype");
+    if (N < 0 || K < 0 || K % block_elems(dtype) != 0)
+        return fail(ctx, TRHIP_ERR_INVALID, "wstore_zero: K must be a non-negative multiple of the block size");
+    DevGuard g(ctx);
+    if (capturing(ctx)) return fail(ctx, TRHIP_ERR_INVALID, "wstore_zero: not allowed while the stream is captured");
+    trhip_wstore *w = nullptr;
+    int st = new_store(ctx, dtype, N, K, &w);
+    if (st != TRHIP_OK) return st;
+    // tensor/quant.go:414-427: every byte 0, except the q4 codes, 0x88 (code 8 opens to (8 - 8) * +0 = +0)
+    const size_t nblk = (size_t)(N * w->nb);
+    st = fill_bytes(ctx, w->base, 0, w->bytes);
+    if (st == TRHIP_OK && dtype == TRHIP_Q4) st = fill_bytes(ctx, w->qs, 0x88, nblk * qs_bytes(dtype));
+    if (st != TRHIP_OK) {
+        drop_store(w);
+        return st;
     }
     *out = w;
     return TRHIP_OK;
@@ -381,29 +652,12 @@ int trhip_wstore_concat(trhip_ctx *ctx, const trhip_wstore *const *parts, int np
         N += p->N;
     }
     DevGuard g(ctx);
-    trhip_wstore *w = new (std::nothrow) trhip_wstore();
-    if (!w) return TRHIP_ERR_OOM;
+    if (capturing(ctx)) return fail(ctx, TRHIP_ERR_INVALID, "wstore_concat: not allowed while the stream is captured");
     const int dtype = p0->dtype;
-    w->ctx = ctx;
-    w->dtype = dtype;
-    w->N = N;
-    w->K = p0->K;
-    w->nb = p0->nb;
-    size_t nblk = (size_t)(N * w->nb);
-    size_t o_aux = align_up(nblk * qs_bytes(dtype), 256);
-    size_t o_sc = align_up(o_aux + nblk * aux_bytes(dtype), 256);
-    size_t o_d = align_up(o_sc + nblk * sc_bytes(dtype), 256);
-    size_t total = align_up(o_d + nblk * d_bytes(dtype), 256);
-    hipError_t e = hipMalloc(&w->base, total ? total : 256);
-    if (e != hipSuccess) {
-        delete w;
-        return hip_fail(ctx, e, "wstore_concat alloc");
-    }
-    w->bytes = total;
-    w->qs = w->base;
-    w->aux = aux_bytes(dtype) ? w->base + o_aux : nullptr;
-    w->sc = sc_bytes(dtype) ? w->base + o_sc : nullptr;
-    w->d = d_bytes(dtype) ? reinterpret_cast<uint16_t *>(w->base + o_d) : nullptr;
+    trhip_wstore *w = nullptr;
+    int st = new_store(ctx, dtype, N, p0->K, &w);
+    if (st != TRHIP_OK) return st;
+    hipError_t e = hipSuccess;
     // every plane is row-major over blocks, so the rows of the parts follow each other plane by plane
     size_t at = 0;
     for (int i = 0; i < nparts && e == hipSuccess; i++) {
@@ -423,9 +677,7 @@ int trhip_wstore_concat(trhip_ctx *ctx, const trhip_wstore *const *parts, int np
         at += nbk;
     }
     if (e != hipSuccess) {
-        (void)hipStreamSynchronize(ctx->stream);
-        (void)hipFree(w->base);
-        delete w;
+        drop_store(w);
         return hip_fail(ctx, e, "wstore_concat copy");
     }
     *out = w;
@@ -435,6 +687,7 @@ int trhip_wstore_concat(trhip_ctx *ctx, const trhip_wstore *const *parts, int np
 int trhip_wstore_destroy(trhip_wstore *w) {
     if (!w) return TRHIP_ERR_INVALID;
     DevGuard g(w->ctx);
+    if (capturing(w->ctx)) return fail(w->ctx, TRHIP_ERR_INVALID, "wstore_destroy: not allowed while the stream is captured");
     (void)hipStreamSynchronize(w->ctx->stream);
     (void)hipFree(w->base);
     delete w;
@@ -456,6 +709,7 @@ int trhip_wstore_to_raw(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int
     size_t bytes = (size_t)(rows * w->nb) * (size_t)block_bytes(w->dtype);
     if (!bytes) return TRHIP_OK;
     DevGuard g(ctx);
+    if (capturing(ctx)) return fail(ctx, TRHIP_ERR_INVALID, "to_raw: waits for the stream; not allowed while it is captured");
     int st = TRHIP_OK;
     uint8_t *stage = static_cast<uint8_t *>(workspace(ctx, bytes, &st));
     if (!stage) return st;
@@ -603,6 +857,12 @@ int trhip_read_probe(trhip_ctx *ctx, const void *p, int64_t bytes) {
     return launch_read_probe(ctx, p, bytes);
 }
 
+int trhip_mfma_probe(trhip_ctx *ctx, int valu_per_mfma, int waves_per_simd, int64_t iters) {
+    if (!ctx) return TRHIP_ERR_INVALID;
+    DevGuard g(ctx);
+    return launch_mfma_probe(ctx, valu_per_mfma, waves_per_simd, iters);
+}
+
 int trhip_embedding_q(trhip_ctx *ctx, const trhip_wstore *w, const int64_t *idx, int64_t nidx, float *out) {
     if (!ctx || !w || nidx < 0) return TRHIP_ERR_INVALID;
     if (nidx == 0) return TRHIP_OK;
@@ -611,11 +871,34 @@ int trhip_embedding_q(trhip_ctx *ctx, const trhip_wstore *w, const int64_t *idx,
         if (idx[i] < 0 || idx[i] >= w->N)
             return fail(ctx, TRHIP_ERR_INVALID, "embedding_q: index " + std::to_string(idx[i]) + " out of range (H3043)");
     DevGuard g(ctx);
+    // The indices go through pinned staging owned by the context, so the upload is asynchronous; the staging is
+    // rewritten only after the copy that last read it has completed. A captured graph would replay whatever the
+    // staging holds then, so host indices are refused during capture.
+    if (capturing(ctx))
+        return fail(ctx, TRHIP_ERR_INVALID, "embedding_q: host indices cannot be captured into a graph");
+    const size_t ib = (size_t)nidx * sizeof(int64_t);
+    hipError_t e = hipSuccess;
+    if (!ctx->idx_done) e = hipEventCreateWithFlags(&ctx->idx_done, hipEventDisableTiming);
+    else e = hipEventSynchronize(ctx->idx_done);
+    if (e != hipSuccess) return hip_fail(ctx, e, "embedding_q: staging event");
+    if (ib > ctx->idx_host_bytes) {
+        if (ctx->idx_host) (void)hipHostFree(ctx->idx_host);
+        ctx->idx_host = nullptr;
+        ctx->idx_host_bytes = 0;
+        const size_t want = ib < 4096 ? 4096 : ib + ib / 4;
+        e = hipHostMalloc(&ctx->idx_host, want, hipHostMallocDefault);
+        if (e != hipSuccess) {
+            ctx->idx_host = nullptr;
+            return hip_fail(ctx, e, "embedding_q: staging alloc");
+        }
+        ctx->idx_host_bytes = want;
+    }
     int st = TRHIP_OK;
-    int64_t *didx = static_cast<int64_t *>(workspace(ctx, (size_t)nidx * sizeof(int64_t), &st));
+    int64_t *didx = static_cast<int64_t *>(workspace(ctx, ib, &st));
     if (!didx) return st;
-    hipError_t e = hipMemcpyAsync(didx, idx, (size_t)nidx * sizeof(int64_t), hipMemcpyHostToDevice, ctx->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);  // idx is caller memory, pageable
+    std::memcpy(ctx->idx_host, idx, ib);
+    e = hipMemcpyAsync(didx, ctx->idx_host, ib, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipEventRecord(ctx->idx_done, ctx->stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "embedding_q: idx upload");
     return launch_embedding(ctx, w, didx, nidx, out, nullptr);
 }

@@ -441,14 +441,9 @@ void launch_exact_t(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t
 }
 
 // Rows per workgroup: the largest of 64, 32, 16 that still gives >= 200 workgroups (64 measured fastest on
-// 14336 rows); TRHIP_GEMV_ROWS (16, 32 or 64) overrides.
-int gemv_rows_per_wg(int64_t N) {
-    static const int forced = [] {
-        const char *e = getenv("TRHIP_GEMV_ROWS");
-        int r = e ? atoi(e) : 0;
-        return (r == 16 || r == 32 || r == 64) ? r : 0;
-    }();
-    if (forced) return forced;
+// 14336 rows); trhip_set_launch_shape(TRHIP_KNOB_EXACT_ROWS) overrides.
+int gemv_rows_per_wg(const trhip_ctx *ctx, int64_t N) {
+    if (ctx->force_exact_rows) return ctx->force_exact_rows;
     if (N >= 64 * 200) return 64;
     if (N >= 32 * 200) return 32;
     return 16;
@@ -461,20 +456,15 @@ int launch_exact(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N,
     if (lds > 160 * 1024) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv: K too large for the LDS copy of x");
     // lanes per row: 8 measured faster for q4_k (14336x4096 cold: 15.7 vs 18.0 us; 1024x4096: 12.5 vs 15.9),
     // q8_0 (4096x4096: 20.3 vs 23.6) and equal for q4_0; 4 stays faster for q6_k (128256x4096: 109 vs 139 us).
-    // TRHIP_EXACT_LANES (4 or 8) overrides.
-    static const int forced = [] {
-        const char *e = getenv("TRHIP_EXACT_LANES");
-        const int v = e ? atoi(e) : 0;
-        return (v == 4 || v == 8) ? v : 0;
-    }();
-    const int lanes = forced ? forced : (DT == kQ6K ? 4 : 8);
+    // trhip_set_launch_shape(TRHIP_KNOB_EXACT_LANES) overrides.
+    const int lanes = ctx->force_exact_lanes ? ctx->force_exact_lanes : (DT == kQ6K ? 4 : 8);
     if (lanes == 8) {
         // 8 lanes per row: 32 rows per 256-thread workgroup, 16 per 128-thread one for small N
         if (N >= 32 * 200) launch_exact8_t<DT, 256>(ctx, w, row0, N, x, c, acc, lds);
         else launch_exact8_t<DT, 128>(ctx, w, row0, N, x, c, acc, lds);
         return launch_check(ctx, "gemv_exact8");
     }
-    switch (gemv_rows_per_wg(N)) {
+    switch (gemv_rows_per_wg(ctx, N)) {
     case 64: launch_exact_t<DT, 256>(ctx, w, row0, N, x, c, acc, lds); break;
     case 32: launch_exact_t<DT, 128>(ctx, w, row0, N, x, c, acc, lds); break;
     default: launch_exact_t<DT, 64>(ctx, w, row0, N, x, c, acc, lds); break;

@@ -660,6 +660,14 @@ int run_q4k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, cons
     size_t lds = (size_t)(nx4 + nx4 / 16) * sizeof(float4) + (size_t)(w->K / 16) * sizeof(float);
     if (lds > 150 * 1024) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv_fast: K too large for the LDS copy of x");
     dim3 grid((unsigned)((N + ROWS - 1) / ROWS)), block(64 * WAVES);
+    if (lds > 62 * 1024) {  // with the kernel's static LDS above 64 KB (K > ~13800): allowed once per device
+        int st = allow_dyn_lds(ctx, reinterpret_cast<const void *>(&gemv_fast_q4k<true, D, WAVES, KS, R>), lds,
+                               "gemv_fast_q4k: LDS size");
+        if (st == TRHIP_OK)
+            st = allow_dyn_lds(ctx, reinterpret_cast<const void *>(&gemv_fast_q4k<false, D, WAVES, KS, R>), lds,
+                               "gemv_fast_q4k: LDS size");
+        if (st != TRHIP_OK) return st;
+    }
     if (acc)
         hipLaunchKernelGGL((gemv_fast_q4k<true, D, WAVES, KS, R>), grid, block, lds, ctx->stream, w->planes(), x, c, N, row0, w->K);
     else
@@ -673,23 +681,21 @@ int launch_gemv(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, 
                 int mode);
 
 namespace {
-// K across lanes with the launch shape "WAVES,KS,PD,RPW" given in TRHIP_KL (read on every call, for tuning), or
-// kNotTaken when TRHIP_KL is not set.
+// K across lanes with the launch shape forced on the context (trhip_set_launch_shape, tests and tuning), or
+// kNotTaken when none is.
 constexpr int kNotTaken = -1;
 template <int DT>
 int kl_forced(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c, bool acc) {
-    const char *kl = getenv("TRHIP_KL");
-    int wv = 0, ks = 0, pd = 0, rpw = 0;
-    if (!kl || sscanf(kl, "%d,%d,%d,%d", &wv, &ks, &pd, &rpw) != 4) return kNotTaken;
-    switch (10000 * wv + 1000 * ks + 10 * pd + rpw / 8) {
-    case 41041: return run_kl<DT, 4, 1, 4, 8>(ctx, w, row0, N, x, c, acc);
-    case 41042: return run_kl<DT, 4, 1, 4, 16>(ctx, w, row0, N, x, c, acc);
-    case 41022: return run_kl<DT, 4, 1, 2, 16>(ctx, w, row0, N, x, c, acc);
-    case 81041: return run_kl<DT, 8, 1, 4, 8>(ctx, w, row0, N, x, c, acc);
-    case 42042: return run_kl<DT, 4, 2, 4, 16>(ctx, w, row0, N, x, c, acc);
-    case 42041: return run_kl<DT, 4, 2, 4, 8>(ctx, w, row0, N, x, c, acc);
-    case 82041: return run_kl<DT, 8, 2, 4, 8>(ctx, w, row0, N, x, c, acc);
-    case 84041: return run_kl<DT, 8, 4, 4, 8>(ctx, w, row0, N, x, c, acc);
+    switch (ctx->force_kl) {
+    case 0: return kNotTaken;
+    case 4141: return run_kl<DT, 4, 1, 4, 8>(ctx, w, row0, N, x, c, acc);
+    case 4142: return run_kl<DT, 4, 1, 4, 16>(ctx, w, row0, N, x, c, acc);
+    case 4122: return run_kl<DT, 4, 1, 2, 16>(ctx, w, row0, N, x, c, acc);
+    case 8141: return run_kl<DT, 8, 1, 4, 8>(ctx, w, row0, N, x, c, acc);
+    case 4242: return run_kl<DT, 4, 2, 4, 16>(ctx, w, row0, N, x, c, acc);
+    case 4241: return run_kl<DT, 4, 2, 4, 8>(ctx, w, row0, N, x, c, acc);
+    case 8241: return run_kl<DT, 8, 2, 4, 8>(ctx, w, row0, N, x, c, acc);
+    case 8441: return run_kl<DT, 8, 4, 4, 8>(ctx, w, row0, N, x, c, acc);
     }
     return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv_kl: no such launch shape");
 }
@@ -727,7 +733,7 @@ int kl_q6k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const
 // shape the unfused fast GEMV takes for 2I rows, so every row sum, and so every gated output, has the same bits
 int launch_gemv_fast_swiglu(trhip_ctx *ctx, const trhip_wstore *w, const float *x, float *out, int64_t I) {
     const int64_t N2 = 2 * I;
-    if (w->dtype != kQ4K || w->N != N2 || getenv("TRHIP_KL") || w->nb < 8 || w->nb > 16) return kNotTaken;
+    if (w->dtype != kQ4K || w->N != N2 || ctx->force_kl || w->nb < 8 || w->nb > 16) return kNotTaken;
     if (N2 >= 10240) return run_kl<kQ4K, 4, 1, 4, 16, true>(ctx, w, 0, I, x, out, false);
     if (N2 >= 6144) return run_kl<kQ4K, 4, 1, 4, 8, true>(ctx, w, 0, I, x, out, false);
     return kNotTaken;
@@ -756,13 +762,8 @@ int launch_gemv_fast(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_
         // rows per lane. Measured on cold 1.1 GiB rings: splitting K wins while the grid is small (1024 / 4096 rows
         // at K = 4096: 5.5 / 5.9 us with 2 parts vs 7.9 / 8.2 whole), whole rows per wave win from ~8192 rows
         // (14336 rows: 10.7-11.5 us vs 11.6-11.7). More blocks in flight or more rows per lane were slower.
-        // TRHIP_FAST_CFG overrides.
-        static const int forced = [] {
-            const char *e = getenv("TRHIP_FAST_CFG");
-            int d = 0, wv = 0, ks = 0, rr = 0;
-            if (e && sscanf(e, "%d,%d,%d,%d", &d, &wv, &ks, &rr) == 4) return 1000 * d + 100 * wv + 10 * ks + rr;
-            return 0;
-        }();
+        // trhip_set_launch_shape(TRHIP_KNOB_FAST_Q4K) overrides.
+        const int forced = ctx->force_fast_q4k;
         // K split in 4 for fewer rows (cold, us): 4096x14336 10.9 vs 14.5 (2 parts), 4096x4096 5.1 vs 6.0,
         // 1024x14336 8.3 vs 12.8
         const int cfg = forced ? forced : (N >= 8192 ? 2411 : (N >= 2048 ? 2841 : 2441));

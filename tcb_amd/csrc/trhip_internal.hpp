@@ -27,6 +27,7 @@
 
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/trhip.h"
 
@@ -182,6 +183,29 @@ struct trhip_ctx {
     // (the merged gate_up output of trhip_gemm_q_swiglu).
     void *ws2 = nullptr;
     size_t ws2_bytes = 0;
+    // Workspace buffers replaced by a larger one while instantiated graphs of this context exist: their kernel
+    // nodes may still hold the old addresses, so the buffers are freed only when the last graph is destroyed
+    // (or with the context).
+    std::vector<void *> retired;
+    int live_graphs = 0;
+    // Pinned host staging for host-side index arrays (trhip_embedding_q): reused once the copy that last read it
+    // has completed (idx_done).
+    void *idx_host = nullptr;
+    size_t idx_host_bytes = 0;
+    hipEvent_t idx_done = nullptr;
+    // Pinned host ring for chunked weight uploads (trhip_wstore_create): UP_SLOTS buffers of up_slot_bytes,
+    // slot s reusable once up_done[s] (recorded after its host-to-device copy) has completed.
+    static constexpr int UP_SLOTS = 2;
+    void *up_host[UP_SLOTS] = {nullptr, nullptr};
+    void *up_dev[UP_SLOTS] = {nullptr, nullptr};
+    hipEvent_t up_done[UP_SLOTS] = {nullptr, nullptr};
+    size_t up_slot_bytes = 0;
+    // Launch-shape overrides set by trhip_set_launch_shape (tests and tuning only); 0 = the built-in choice.
+    int force_kl = 0;           // K-across-lanes GEMV: 1000 WAVES + 100 KS + 10 PD + RPW / 8
+    int force_fast_q4k = 0;     // row-sliced fast q4_k GEMV: 1000 D + 100 WAVES + 10 KS + R
+    int force_exact_rows = 0;   // exact four-lane GEMV rows per workgroup (16, 32, 64)
+    int force_exact_lanes = 0;  // exact GEMV lanes per row (4, 8)
+    int force_actq_tm = 0;      // act-quant MFMA row tile (32, 64)
     int sm_count = 0;
 };
 
@@ -203,9 +227,15 @@ int hip_fail(trhip_ctx *ctx, hipError_t e, const char *what);
 int launch_check(trhip_ctx *ctx, const char *what);
 void *workspace(trhip_ctx *ctx, size_t bytes, int *status);
 void *workspace2(trhip_ctx *ctx, size_t bytes, int *status);
+// Allow `bytes` of dynamic LDS for kernel `fn` on the context's device (needed above 64 KB); done once per device
+// and kernel, thread-safe.
+int allow_dyn_lds(trhip_ctx *ctx, const void *fn, size_t bytes, const char *what);
+// Whether the context's stream is being captured into a graph.
+bool capturing(trhip_ctx *ctx);
 
 // Kernel launchers (one per source file). All return TRHIP_OK or an error code.
-int launch_repack(trhip_ctx *ctx, trhip_wstore *w, const uint8_t *raw_dev);
+// GGUF blocks [block0, block0 + nblocks) of the store, held in raw_dev from its start, into the planes.
+int launch_repack(trhip_ctx *ctx, trhip_wstore *w, const uint8_t *raw_dev, int64_t block0, int64_t nblocks);
 int launch_swiglu(trhip_ctx *ctx, const float *gu, int64_t M, int64_t I, float *out);
 int launch_unpack(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t rows, uint8_t *raw_dev);
 int launch_dequant(trhip_ctx *ctx, const trhip_wstore *w, int64_t block0, int64_t nblocks, float *out);
@@ -226,6 +256,7 @@ int launch_gemm_rows_fast(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, i
 int launch_quantize_q8(trhip_ctx *ctx, const float *x, int64_t M, int64_t K, int blk, int8_t *q, float *d,
                        int16_t *bs, uint8_t *bad, uint16_t *sj);
 int launch_read_probe(trhip_ctx *ctx, const void *p, int64_t bytes);
+int launch_mfma_probe(trhip_ctx *ctx, int valu_per_mfma, int waves_per_simd, int64_t iters);
 int launch_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                 int64_t M, bool acc, const int8_t *q, const float *d, const int16_t *bs, const uint8_t *bad,
                 const uint16_t *sj);

@@ -20,34 +20,121 @@ __host__ __device__ inline int q6k_qh_dst(int i) {  // old = 32n + 8t + l -> 16t
     return 16 * t + 8 * n + l;
 }
 
+// Inverse maps: repacked position j of a q4_k qs / q6_k ql / q6_k qh byte -> its byte in the GGUF block field.
+__host__ __device__ inline int q4k_src(int j) {  // j = 64a + 16g + 8h + l -> 32g + 16a + 8h + l
+    return 32 * ((j >> 4) & 3) + 16 * (j >> 6) + (j & 15);
+}
+__host__ __device__ inline int q6k_ql_src(int j) {  // j = 32t + 16n + 8h + l -> 64n + 32h + 8t + l
+    int t = j >> 5, n = (j >> 4) & 1, h = (j >> 3) & 1, l = j & 7;
+    return 64 * n + 32 * h + 8 * t + l;
+}
+__host__ __device__ inline int q6k_qh_src(int j) {  // j = 16t + 8n + l -> 32n + 8t + l
+    int t = j >> 4, n = (j >> 3) & 1, l = j & 7;
+    return 32 * n + 8 * t + l;
+}
+
+// Fields of a GGUF block as planes (trhip_internal.hpp): plane k holds PB[k] bytes per block. Plane 0 is qs (q6_k ql),
+// then aux (q4_k hdr, q6_k qh), sc, d, in that order for the planes a dtype has.
 template <int DT>
-__global__ void repack_kernel(const uint8_t *__restrict__ raw, uint8_t *__restrict__ qs, uint8_t *__restrict__ aux,
-                              uint8_t *__restrict__ sc, uint16_t *__restrict__ d, int64_t nblocks, bool inverse) {
-    int64_t bi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (bi >= nblocks) return;
-    uint8_t *rb = const_cast<uint8_t *>(raw) + bi * block_bytes(DT);
-    uint8_t *q = qs + bi * qs_bytes(DT);
-    // `inverse` swaps source and destination of every byte move.
-    auto mv = [&](uint8_t *plane_byte, uint8_t *raw_byte) {
-        if (inverse) *raw_byte = *plane_byte; else *plane_byte = *raw_byte;
-    };
-    if (DT == kQ8 || DT == kQ4) {
-        uint8_t *dd = reinterpret_cast<uint8_t *>(d + bi);
-        mv(dd, rb);
-        mv(dd + 1, rb + 1);
-        for (int i = 0; i < qs_bytes(DT); i++) mv(q + i, rb + 2 + i);
-    } else if (DT == kQ4K) {
-        uint8_t *h = aux + bi * 16;
-        for (int i = 0; i < 16; i++) mv(h + i, rb + i);
-        for (int i = 0; i < 128; i++) mv(q + q4k_pos(i), rb + 16 + i);
-    } else {  // q6_k: ql[128] qh[64] sc[16] d[2]
-        uint8_t *h = aux + bi * 64, *s = sc + bi * 16;
-        uint8_t *dd = reinterpret_cast<uint8_t *>(d + bi);
-        for (int i = 0; i < 128; i++) mv(q + q6k_ql_dst(i), rb + i);
-        for (int i = 0; i < 64; i++) mv(h + q6k_qh_dst(i), rb + 128 + i);
-        for (int i = 0; i < 16; i++) mv(s + i, rb + 192 + i);
-        mv(dd, rb + 208);
-        mv(dd + 1, rb + 209);
+struct Fields {
+    static constexpr int NP = DT == kQ6K ? 4 : 2;
+    static constexpr int pb(int k) {
+        return DT == kQ8 ? (k == 0 ? 32 : 2)
+             : DT == kQ4 ? (k == 0 ? 16 : 2)
+             : DT == kQ4K ? (k == 0 ? 128 : 16)
+                          : (k == 0 ? 128 : k == 1 ? 64 : k == 2 ? 16 : 2);
+    }
+    // GGUF block byte of plane k's byte j
+    __device__ static int raw_of(int k, int j) {
+        if (DT == kQ8 || DT == kQ4) return k == 0 ? 2 + j : j;
+        if (DT == kQ4K) return k == 0 ? 16 + q4k_src(j) : j;
+        return k == 0 ? q6k_ql_src(j) : k == 1 ? 128 + q6k_qh_src(j) : k == 2 ? 192 + j : 208 + j;
+    }
+    // plane and plane byte of GGUF block byte r
+    __device__ static void plane_of(int r, int &k, int &j) {
+        if (DT == kQ8 || DT == kQ4) { k = r < 2 ? 1 : 0; j = r < 2 ? r : r - 2; }
+        else if (DT == kQ4K) { k = r < 16 ? 1 : 0; j = r < 16 ? r : q4k_pos(r - 16); }
+        else if (r < 128) { k = 0; j = q6k_ql_dst(r); }
+        else if (r < 192) { k = 1; j = q6k_qh_dst(r - 128); }
+        else if (r < 208) { k = 2; j = r - 192; }
+        else { k = 3; j = r - 208; }
+    }
+};
+
+// LDS <- bytes of global memory: 16-byte loads where the source is aligned and whole, else byte loads. dst is
+// 16-byte aligned.
+__device__ __forceinline__ void load_lds(uint8_t *dst, const uint8_t *__restrict__ src, int bytes) {
+    for (int u = threadIdx.x; 16 * u < bytes; u += blockDim.x) {
+        const uint8_t *s = src + 16 * u;
+        if (16 * u + 16 <= bytes && reinterpret_cast<uintptr_t>(s) % 16 == 0) {
+            *reinterpret_cast<uint4 *>(dst + 16 * u) = *reinterpret_cast<const uint4 *>(s);
+        } else {
+            for (int k = 0; k < 16 && 16 * u + k < bytes; k++) dst[16 * u + k] = s[k];
+        }
+    }
+}
+
+// bytes [0, bytes) of dst <- a gather from LDS: byte o comes from lds[at(o)]. 16-byte stores where dst is aligned
+// and the unit whole, else byte stores.
+template <typename F>
+__device__ __forceinline__ void store_gather(uint8_t *__restrict__ dst, int bytes, const uint8_t *lds, F at) {
+    for (int u = threadIdx.x; 16 * u < bytes; u += blockDim.x) {
+        uint8_t *d = dst + 16 * u;
+        if (16 * u + 16 <= bytes && reinterpret_cast<uintptr_t>(d) % 16 == 0) {
+            uint32_t wd[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                uint32_t v = 0;
+#pragma unroll
+                for (int k = 0; k < 4; k++) v |= (uint32_t)lds[at(16 * u + 4 * q + k)] << (8 * k);
+                wd[q] = v;
+            }
+            *reinterpret_cast<uint4 *>(d) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+        } else {
+            for (int k = 0; k < 16 && 16 * u + k < bytes; k++) d[k] = lds[at(16 * u + k)];
+        }
+    }
+}
+
+// Repack (GGUF blocks -> planes) or, with INV, unpack (planes -> GGUF blocks) of blocks [block0, block0 + nblocks)
+// of a store; raw holds those blocks from its start. A workgroup takes RB consecutive blocks: it reads their source
+// bytes into LDS with coalesced 16-byte loads and writes each destination region with coalesced 16-byte stores,
+// gathering the bytes from LDS (a byte permutation, nothing is decoded).
+constexpr int RB = 64;
+template <int DT, bool INV>
+__global__ __launch_bounds__(256) void repack_kernel(uint8_t *__restrict__ raw, uint8_t *__restrict__ qs,
+                                                     uint8_t *__restrict__ aux, uint8_t *__restrict__ sc,
+                                                     uint8_t *__restrict__ d, int64_t block0, int64_t nblocks) {
+    using F = Fields<DT>;
+    constexpr int BB = block_bytes(DT);
+    __shared__ __align__(16) uint8_t lds[RB * BB + 64];
+    const int64_t g0 = (int64_t)blockIdx.x * RB;  // first block of this workgroup, relative to block0
+    const int nbk = (int)(nblocks - g0 < RB ? nblocks - g0 : RB);
+    uint8_t *planes[4] = {qs, aux, sc, d};
+    uint8_t *rg = raw + g0 * BB;
+    if (!INV) {
+        load_lds(lds, rg, nbk * BB);
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < F::NP; k++) {
+            const int pb = F::pb(k);
+            store_gather(planes[k] + (block0 + g0) * pb, nbk * pb, lds,
+                         [&](int o) { return (o / pb) * BB + F::raw_of(k, o % pb); });
+        }
+    } else {
+        int base[4], at = 0;
+#pragma unroll
+        for (int k = 0; k < F::NP; k++) {  // plane sections of the group in LDS, each 16-byte aligned
+            base[k] = at;
+            load_lds(lds + at, planes[k] + (block0 + g0) * F::pb(k), nbk * F::pb(k));
+            at += (nbk * F::pb(k) + 15) / 16 * 16;
+        }
+        __syncthreads();
+        store_gather(rg, nbk * BB, lds, [&](int o) {
+            int k, j;
+            F::plane_of(o % BB, k, j);
+            return base[k] + (o / BB) * F::pb(k) + j;
+        });
     }
 }
 
@@ -143,12 +230,16 @@ template <int DT>
 struct RepackRun {
     static int run(trhip_ctx *ctx, const trhip_wstore *w, uint8_t *raw, int64_t block0, int64_t nblocks, bool inv) {
         if (nblocks == 0) return TRHIP_OK;
-        const int threads = 256;
-        int64_t grid = (nblocks + threads - 1) / threads;
-        hipLaunchKernelGGL(repack_kernel<DT>, dim3((unsigned)grid), dim3(threads), 0, ctx->stream, raw,
-                           w->qs + block0 * qs_bytes(DT), w->aux ? w->aux + block0 * aux_bytes(DT) : nullptr,
-                           w->sc ? w->sc + block0 * sc_bytes(DT) : nullptr, w->d ? w->d + block0 : nullptr, nblocks,
-                           inv);
+        const int64_t grid = (nblocks + RB - 1) / RB;
+        if (grid >= ((int64_t)1 << 31)) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "repack: too many blocks");
+        uint8_t *d8 = reinterpret_cast<uint8_t *>(w->d);
+        uint8_t *p1 = DT == kQ8 || DT == kQ4 ? d8 : w->aux, *p2 = w->sc, *p3 = DT == kQ6K ? d8 : nullptr;
+        if (inv)
+            hipLaunchKernelGGL((repack_kernel<DT, true>), dim3((unsigned)grid), dim3(256), 0, ctx->stream, raw, w->qs,
+                               p1, p2, p3, block0, nblocks);
+        else
+            hipLaunchKernelGGL((repack_kernel<DT, false>), dim3((unsigned)grid), dim3(256), 0, ctx->stream, raw, w->qs,
+                               p1, p2, p3, block0, nblocks);
         return launch_check(ctx, inv ? "unpack" : "repack");
     }
 };
@@ -182,9 +273,9 @@ struct EmbedRun {
 
 }  // namespace
 
-int launch_repack(trhip_ctx *ctx, trhip_wstore *w, const uint8_t *raw_dev) {
-    return dispatch_dt<RepackRun>(w->dtype, ctx, (const trhip_wstore *)w, const_cast<uint8_t *>(raw_dev), (int64_t)0,
-                                  w->N * w->nb, false);
+int launch_repack(trhip_ctx *ctx, trhip_wstore *w, const uint8_t *raw_dev, int64_t block0, int64_t nblocks) {
+    return dispatch_dt<RepackRun>(w->dtype, ctx, (const trhip_wstore *)w, const_cast<uint8_t *>(raw_dev), block0,
+                                  nblocks, false);
 }
 
 int launch_unpack(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t rows, uint8_t *raw_dev) {

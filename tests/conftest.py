@@ -39,3 +39,17 @@ def backend():
     b = QuantBackend(0)
     yield b
     b.close()
+
+
+@pytest.fixture
+def launch_shape(backend):
+    """force(knob, a, b, c, d) forces a launch shape on the session context; every knob is reset afterwards."""
+    used = []
+
+    def force(knob, *vals):
+        backend.ctx.set_launch_shape(knob, *vals)
+        used.append(knob)
+
+    yield force
+    for k in used:
+        backend.ctx.set_launch_shape(k)

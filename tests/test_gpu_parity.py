@@ -5,12 +5,15 @@ the fp32 GEMV (quantDot = dequant + sdot32), the M>1 chunk order (quantGemmPanel
 the act-quant block kernels (cpu_quant_q8.go Go twins). Shapes follow the reference's own tests
 (cpu_quant_test.go, cpu_quant_q8_test.go, gpu/behavior_quant_test.go) plus the Llama-3-8B shapes.
 """
+import functools
+
 import numpy as np
 import pytest
 
 import oracle as O
 from conftest import rel_err, same_bits
 from tcb_amd import BLOCK, MODE_EXACT, MODE_FAST, Q4, Q4K, Q6K, Q8, TrhipError
+from tcb_amd._lib import KNOB_KL
 from tcb_amd import synth
 
 pytestmark = pytest.mark.gpu
@@ -41,6 +44,69 @@ def test_store_round_trip(backend, dt):
     rb = raw.size // N
     assert np.array_equal(w.ToRaw(5, 11), raw[5 * rb:16 * rb])
     w.release()
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_store_chunked_upload(backend, dt):
+    """A store larger than one 32 MiB upload slot (several chunks, a ragged last one) from pageable and from pinned
+    host memory: ToRaw gives the GGUF bytes back and OpenQuant equals the oracle's dequantization."""
+    elems, size = BLOCK[dt]
+    K = 4096
+    N = (70 << 20) // (K // elems * size) + 3
+    raw = O.random_quant(dt, 7, N * K // elems)
+    w = backend.FromQuantized(dt, raw, N, K)
+    assert np.array_equal(w.ToRaw(), raw)
+    h, p = backend.ctx.host_alloc(raw.nbytes)
+    h[:] = raw
+    w2 = backend.FromQuantized(dt, h, N, K)
+    backend.ctx.host_free(p)
+    assert np.array_equal(w2.ToRaw(N - 5, 5), raw[-5 * (K // elems) * size:])
+    rows = 300
+    out = backend.ctx.alloc(rows * K * 4)
+    backend.OpenQuant(out, w2, offset=(N - rows) * K, n=rows * K)
+    same_bits(out.download(np.float32, rows * K), O.dequant(dt, raw[-rows * (K // elems) * size:]))
+    out.free()
+    w.release()
+    w2.release()
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_zero_store(backend, dt):
+    """NewQuantStorage (tensor/quant.go:408-427): the GGUF bytes are QuantZeroRaw's (q4 codes 0x88) and OpenQuant and
+    a GEMV over them give the oracle's bits. Every element is zero: +0 for q8, q4 and q4_k; q6_k opens to -0, as the
+    reference's own dequantQ6K computes it (d * sc * (0 - 32) = +0 * -32, tensor/quant.go:197)."""
+    elems, _ = BLOCK[dt]
+    N, K = 33, 4 * elems * 2
+    zero = O.quant_zero_raw(dt, N * K)
+    w = backend.NewQuantStorage(dt, N, K)
+    assert np.array_equal(w.ToRaw(), zero)
+    out = backend.ctx.alloc(N * K * 4)
+    backend.OpenQuant(out, w)
+    y = out.download(np.float32, N * K)
+    same_bits(y, O.dequant(dt, zero))
+    assert not np.any(y)
+    if dt != Q6K:
+        assert not y.view(np.uint32).any()  # +0 bits
+    x = synth.activations(1, K, seed=1)
+    xb, cb = backend.ctx.to_device(x), backend.ctx.to_device(np.ones(N, np.float32))
+    backend.GemmSet(1, N, K, xb, w, cb)
+    same_bits(cb.download(np.float32, N), O.quant_gemm(dt, 1, N, K, x, zero).reshape(-1))
+    for b in (out, xb, cb):
+        b.free()
+    w.release()
+
+
+def test_memset_kernel(backend):
+    """trhip_memset_async is a fill kernel: any offset and length, bytes outside the range untouched."""
+    buf = backend.ctx.to_device(np.full(4096, 0x11, np.uint8))
+    for off, n, v in ((0, 4096, 0), (3, 1000, 0xAB), (17, 1, 0x5C), (64, 2048, 0xFF)):
+        want = buf.download(np.uint8, 4096).copy()
+        want[off:off + n] = v
+        backend.ctx.sync()
+        from tcb_amd import _lib
+        assert _lib.lib().trhip_memset_async(backend.ctx.h, buf.addr(off), v, n) == 0
+        assert np.array_equal(buf.download(np.uint8, 4096), want)
+    buf.free()
 
 
 @pytest.mark.parametrize("dt,seed,want,at,sample", [
@@ -344,20 +410,62 @@ def test_gemm_rows_llama_shapes_bits(backend, dt, N, K, M):
     w.release()
 
 
+@functools.lru_cache(maxsize=2)
+def _ffn_q4k(N, K):
+    return synth.quant_weights(Q4K, N, K, seed=41, outliers=0.01)
+
+
 @pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336)])
 @pytest.mark.parametrize("M", [128, 512, 2048])
 def test_actq_prefill_sizes_bits(backend, N, K, M):
-    """The prefill configurations (q4_k, M in {128, 512, 2048}). Every output row is one single-row kernel result
-    (cpu_quant_q8.go:183-185), so at M = 128 all rows are compared and above that a fixed sample of rows."""
-    raw = synth.quant_weights(Q4K, N, K, seed=41, outliers=0.01)
+    """The prefill configurations (q4_k, M in {128, 512, 2048}), every output row and column compared: each is one
+    single-row kernel result (cpu_quant_q8.go:183-185), bit-identical."""
+    raw = _ffn_q4k(N, K)
     X = synth.activations(M, K, seed=42 + M)
     w = backend.FromQuantized(Q4K, raw, N, K)
     xb, cb = backend.ctx.to_device(X), backend.ctx.alloc(M * N * 4)
     backend.GemmActQuant(M, N, K, xb, w, cb, accumulate=False)
     got = cb.download(np.float32, M * N).reshape(M, N)
-    rows = list(range(M)) if M <= 128 else sorted({0, 1, 63, 64, 127, M // 2 + 3, M - 65, M - 2, M - 1})
-    want = O.quant_gemm_act(Q4K, len(rows), N, K, np.ascontiguousarray(X[rows]), raw)
-    same_bits(got[rows], want)
+    same_bits(got, O.quant_gemm_act(Q4K, M, N, K, X, raw))
+    for b in (xb, cb):
+        b.free()
+    w.release()
+
+
+@pytest.mark.parametrize("dt", DTS)
+@pytest.mark.parametrize("M", [97, 128])
+def test_gemm_rows_above_panel_bits(backend, dt, M):
+    """M > 96 takes the reference's other M > 1 driver (cpu_quant.go:59-82, quantGemm without panels); it keeps the
+    256-deep chunk order per output, so the result is the same bits as below 96 rows (TestQuantMatMulSameBitsAsOpened
+    at a larger M)."""
+    N, K = 300, 4096
+    raw = synth.quant_weights(dt, N, K, seed=61 + M, outliers=0.01 if dt in (Q4K, Q6K) else 0.0)
+    X = synth.activations(M, K, seed=62)
+    X[5] *= 1000
+    w = backend.FromQuantized(dt, raw, N, K)
+    c0 = synth.activations(M, N, seed=63).reshape(-1)
+    xb, cb = backend.ctx.to_device(X), backend.ctx.to_device(c0)
+    backend.Gemm(M, N, K, xb, w, cb)
+    same_bits(cb.download(np.float32, M * N), O.quant_gemm(dt, M, N, K, X, raw, c0))
+    for b in (xb, cb):
+        b.free()
+    w.release()
+
+
+@pytest.mark.parametrize("dt", [Q4K, Q6K])
+def test_gemv_k16384(backend, dt):
+    """K = 16384, the largest K the fast M == 1 kernels take (four K parts of 16 blocks): exact bit-identical, fast
+    within the bound."""
+    N, K = 500, 16384
+    raw = synth.quant_weights(dt, N, K, seed=71, outliers=0.01)
+    x = synth.activations(1, K, seed=72)
+    w = backend.FromQuantized(dt, raw, N, K)
+    xb, cb = backend.ctx.to_device(x), backend.ctx.alloc(N * 4)
+    want = O.quant_gemm(dt, 1, N, K, x, raw).reshape(-1)
+    backend.GemmSet(1, N, K, xb, w, cb, mode=MODE_EXACT)
+    same_bits(cb.download(np.float32, N), want)
+    backend.GemmSet(1, N, K, xb, w, cb, mode=MODE_FAST)
+    assert rel_err(cb.download(np.float32, N), want) <= FAST_TOL[dt]
     for b in (xb, cb):
         b.free()
     w.release()
@@ -392,7 +500,14 @@ def test_embedding(backend, dt):
     same_bits(out1.download(np.float32, len(idx) * D, byte_offset=4), O.embedding(dt, raw, D, idx))
     with pytest.raises(TrhipError):
         backend.Embedding(out, w, [5])
-    for b in (out, out1):
+    # back-to-back lookups with no sync between them: the pinned index staging is reused only after its copy ran
+    outs = [backend.ctx.alloc(3 * D * 4) for _ in range(4)]
+    picks = [[1, 2, 3], [3, 3, 0], [4, 1, 2], [0, 0, 0]]
+    for o, ix in zip(outs, picks):
+        backend.Embedding(o, w, ix)
+    for o, ix in zip(outs, picks):
+        same_bits(o.download(np.float32, 3 * D), O.embedding(dt, raw, D, ix))
+    for b in [out, out1] + outs:
         b.free()
     w.release()
 
@@ -478,7 +593,7 @@ def test_gemv_fast_deterministic_and_sliced(backend, dt):
     w.release()
 
 
-# q4_k fast GEMV with K across lanes (fixed-point x, int8 dot products); TRHIP_KL forces a launch shape
+# q4_k fast GEMV with K across lanes (fixed-point x, int8 dot products); the launch_shape fixture forces a shape
 KL_SHAPES = ["4,1,4,8", "4,1,4,16", "4,1,2,16", "8,1,4,8", "4,2,4,16", "8,4,4,8"]
 
 
@@ -489,11 +604,11 @@ def _kl_parts(cfg):
 @pytest.mark.parametrize("cfg", KL_SHAPES)
 @pytest.mark.parametrize("N,K,row0", [(1, 256, 0), (37, 1024, 0), (300, 4096, 5), (129, 3840, 0), (9000, 4096, 100),
                                       (70, 14336, 3), (40, 8192, 0)])
-def test_gemv_kl_tolerance(backend, monkeypatch, cfg, N, K, row0):
+def test_gemv_kl_tolerance(backend, launch_shape, cfg, N, K, row0):
     """Every launch shape of the K-across-lanes kernel on ragged shapes (rows fewer than row groups, partial K
     parts, a row slice), set and accumulate, x1 and x1000 activations: within 1e-4 of the oracle. Shapes whose
     K needs more than 16 blocks per part are refused."""
-    monkeypatch.setenv("TRHIP_KL", cfg)
+    launch_shape(KNOB_KL, *map(int, cfg.split(",")))
     rows = N
     raw = synth.quant_weights(Q4K, N + row0, K, seed=N + K, outliers=0.01)
     w = backend.FromQuantized(Q4K, raw, N + row0, K)
@@ -524,10 +639,10 @@ def test_gemv_kl_tolerance(backend, monkeypatch, cfg, N, K, row0):
 
 
 @pytest.mark.parametrize("cfg", ["4,1,4,16", "8,4,4,8"])
-def test_gemv_kl_activation_range(backend, monkeypatch, cfg):
+def test_gemv_kl_activation_range(backend, launch_shape, cfg):
     """Fixed-point x is scaled per 32-element half: one huge element among tiny ones, an all-zero half, and
     subnormal activations stay within tolerance (zero x gives zero rows)."""
-    monkeypatch.setenv("TRHIP_KL", cfg)
+    launch_shape(KNOB_KL, *map(int, cfg.split(",")))
     N, K = 64, 4096 if _kl_parts(cfg) == 1 else 14336
     raw = synth.quant_weights(Q4K, N, K, seed=8, outliers=0.01)
     w = backend.FromQuantized(Q4K, raw, N, K)
@@ -560,10 +675,10 @@ def test_gemv_kl_activation_range(backend, monkeypatch, cfg):
 
 @pytest.mark.parametrize("cfg", ["4,1,4,16", "8,4,4,8"])
 @pytest.mark.parametrize("bad", [np.inf, -np.inf, np.nan])
-def test_gemv_kl_non_finite(backend, monkeypatch, cfg, bad):
+def test_gemv_kl_non_finite(backend, launch_shape, cfg, bad):
     """Inf or NaN in x takes float products in the lanes that hold it: every row is NaN or +-Inf exactly where the
     bit-exact GEMV is (a zero weight times Inf is NaN, as on the CPU)."""
-    monkeypatch.setenv("TRHIP_KL", cfg)
+    launch_shape(KNOB_KL, *map(int, cfg.split(",")))
     N, K = 48, 4096 if _kl_parts(cfg) == 1 else 14336
     raw = synth.quant_weights(Q4K, N, K, seed=4, outliers=0.01)
     w = backend.FromQuantized(Q4K, raw, N, K)
@@ -893,11 +1008,11 @@ def test_gemv_fast_q8_q4(backend, dt, N, K):
 @pytest.mark.parametrize("dt", [Q8, Q4, Q6K])
 @pytest.mark.parametrize("cfg", ["4,1,4,8", "4,1,4,16", "4,1,2,16", "8,1,4,8", "4,2,4,16", "4,2,4,8", "8,2,4,8",
                                  "8,4,4,8"])
-def test_gemv_fast_q8_q4_launch_shapes(backend, monkeypatch, dt, cfg):
+def test_gemv_fast_q8_q4_launch_shapes(backend, launch_shape, dt, cfg):
     """Every launch shape of the K-across-lanes kernel for q8_0 / q4_0 / q6_k on ragged rows and K parts (K = 8192
     and 2560: parts of up to 128 blocks of 32, or 16 of 256), within the bound; shapes whose parts exceed that are
     refused."""
-    monkeypatch.setenv("TRHIP_KL", cfg)
+    launch_shape(KNOB_KL, *map(int, cfg.split(",")))
     ks = int(cfg.split(",")[1])
     for N, K in ((133, 8192), (70, 2560)):
         raw = synth.quant_weights(dt, N, K, seed=N + K, outliers=0.01 if dt == Q6K else 0.0)
@@ -969,3 +1084,14 @@ def test_read_probe(backend):
         backend.ctx.read_probe(buf, 100)
     assert e.value.code == 1
     buf.free()
+
+
+def test_mfma_probe(backend):
+    """The int8 matrix-core diagnostic runs for every VALU mix it has and refuses others."""
+    from tcb_amd import _lib
+    L = _lib.lib()
+    for v in (0, 2, 4, 6, 8, 12, 16):
+        assert L.trhip_mfma_probe(backend.ctx.h, v, 2, 8) == 0
+    assert L.trhip_mfma_probe(backend.ctx.h, 5, 2, 8) == 1
+    assert L.trhip_mfma_probe(backend.ctx.h, 0, 5, 8) == 1
+    backend.ctx.sync()
