@@ -150,6 +150,18 @@ int trhip_gemm_q(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N,
 int trhip_gemm_q_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x,
                       float *c, int64_t M, int64_t K, int accumulate);
 
+/* No counterpart in the reference: trhip_gemm_q_actq for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same arguments, kernels and bits as
+ * trhip_gemm_q_actq, but the quantized activations live in a static device array of
+ * TRHIP_NOALLOC_SCRATCH_BYTES per device instead of the context's workspace, and nothing is allocated or freed.
+ * Shapes whose scratch exceeds it (about 1.27 M*K bytes, plus 4 M*K when x is not 16-byte aligned; M = 2048 at
+ * K = 14336 fits) fail with TRHIP_ERR_INVALID before anything runs. Every call on one device shares that array:
+ * calls that overlap on one device (two contexts, or two streams) race. No part of the array needs to start at
+ * zero. */
+#define TRHIP_NOALLOC_SCRATCH_BYTES (40u << 20)
+int trhip_gemm_q_actq_noalloc(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x,
+                              float *c, int64_t M, int64_t K, int accumulate);
+
 /* QuantOpener.OpenQuant (tensor/quant.go:103-105, gpu/backend_quant.go:117-134): elements
  * [elem_off, elem_off+n) of the store in row-major order, dequantized to fp32, bit-identical
  * to tensor/quant.go:139-205. elem_off and n must be multiples of the block size. */

@@ -48,6 +48,7 @@ SIGNATURES = [
     ("trhip_wstore_concat", INT, [P, P, INT, ctypes.POINTER(P)]),
     ("trhip_gemm_q", INT, [P, P, I64, I64, P, P, I64, I64, INT, INT]),
     ("trhip_gemm_q_actq", INT, [P, P, I64, I64, P, P, I64, I64, INT]),
+    ("trhip_gemm_q_actq_noalloc", INT, [P, P, I64, I64, P, P, I64, I64, INT]),
     ("trhip_open_q", INT, [P, P, I64, I64, P]),
     ("trhip_read_probe", INT, [P, P, I64]),
     ("trhip_mfma_probe", INT, [P, INT, INT, I64]),

@@ -142,6 +142,8 @@ struct DevGuard {  // bind the context's device for the duration of a call (gpu/
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+int scratch_dev(trhip_ctx *ctx);  // below, beside the static scratch array
+
 bool bad_scale16(const uint8_t *p) { return ((p[0] | (p[1] << 8)) & 0x7C00) == 0x7C00; }
 
 }  // namespace
@@ -198,6 +200,13 @@ int trhip_init(int device, trhip_ctx **out) {
     }
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, device) == hipSuccess) ctx->sm_count = prop.multiProcessorCount;
+    const int st = scratch_dev(ctx);
+    if (st != TRHIP_OK) {
+        g_noctx_err = ctx->err;
+        (void)hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return st;
+    }
     *out = ctx;
     return TRHIP_OK;
 }
@@ -795,46 +804,125 @@ int trhip_quantize_q8(trhip_ctx *ctx, const float *x, int64_t M, int64_t K, int 
     return launch_quantize_q8(ctx, x, M, K, blk, q, d, bs, bad, nullptr);
 }
 
-int trhip_gemm_q_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
-                      int64_t M, int64_t K, int accumulate) {
-    if (!ctx || !w) return TRHIP_ERR_INVALID;
-    if (w->dtype == TRHIP_Q8) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemm_q_actq: q8 weights are not supported (H6723)");
+}  // extern "C"
+
+namespace {
+
+// Scratch layout of the act-quant operator: q [M][K] int8, d [M][K/blk] fp32, bs [M][K/16] int16, one NaN/Inf flag
+// byte per activation block, for q4_k the f16 msum operands [M][K/256][16], and an aligned copy of x when x is not
+// 16-byte aligned.
+struct ActqLayout {
+    size_t o_q = 0, o_d = 0, o_bs = 0, o_fl = 0, o_sj = 0, o_x = 0, total = 0;
+    bool copy_x = false;
+};
+
+ActqLayout actq_layout(int dtype, int64_t M, int64_t K, const float *x) {
+    ActqLayout l;
+    const int64_t nb = K / block_elems(dtype);
+    l.o_d = align_up(l.o_q + (size_t)(M * K), 256);
+    l.o_bs = align_up(l.o_d + (size_t)(M * nb) * sizeof(float), 256);
+    l.o_fl = align_up(l.o_bs + (size_t)(M * (K / 16)) * sizeof(int16_t), 256);
+    l.o_sj = align_up(l.o_fl + (size_t)(M * nb), 256);
+    l.o_x = align_up(l.o_sj + (dtype == TRHIP_Q4K ? (size_t)(M * nb) * 32 : 0), 256);
+    l.copy_x = reinterpret_cast<uintptr_t>(x) % 16 != 0;
+    l.total = l.o_x + (l.copy_x ? (size_t)(M * K) * sizeof(float) : 0);
+    return l;
+}
+
+// Argument checks shared by both act-quant entry points; 0 = go on, 1 = done (nothing to compute), else a status.
+int actq_check(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c, int64_t M,
+               int64_t K, const char *name, int *status) {
+    *status = TRHIP_OK;
+    if (w->dtype == TRHIP_Q8)
+        return *status = fail(ctx, TRHIP_ERR_UNSUPPORTED, std::string(name) + ": q8 weights are not supported (H6723)"), 2;
     if (M < 0 || N < 0 || row0 < 0 || row0 + N > w->N || K != w->K)
-        return fail(ctx, TRHIP_ERR_INVALID, "gemm_q_actq: shape does not match the store");
-    if (M == 0 || N == 0) return TRHIP_OK;
-    DevGuard g(ctx);
-    if (K == 0) {
-        if (accumulate) return TRHIP_OK;
-        return zero_f32(ctx, c, M * N);
-    }
-    if (!x || !c) return fail(ctx, TRHIP_ERR_INVALID, "gemm_q_actq: null x or c");
-    int blk = block_elems(w->dtype);
-    int64_t nb = K / blk;
-    size_t o_q = 0;
-    size_t o_d = align_up(o_q + (size_t)(M * K), 256);
-    size_t o_bs = align_up(o_d + (size_t)(M * nb) * sizeof(float), 256);
-    size_t o_fl = align_up(o_bs + (size_t)(M * (K / 16)) * sizeof(int16_t), 256);
-    size_t o_sj = align_up(o_fl + (size_t)(M * nb), 256);
-    size_t o_x = align_up(o_sj + (w->dtype == TRHIP_Q4K ? (size_t)(M * nb) * 32 : 0), 256);
-    bool copy_x = reinterpret_cast<uintptr_t>(x) % 16 != 0;
-    size_t total = o_x + (copy_x ? (size_t)(M * K) * sizeof(float) : 0);
-    int st = TRHIP_OK;
-    uint8_t *ws = static_cast<uint8_t *>(workspace(ctx, total, &st));
-    if (!ws) return st;
-    int8_t *q = reinterpret_cast<int8_t *>(ws + o_q);
-    float *d = reinterpret_cast<float *>(ws + o_d);
-    int16_t *bs = reinterpret_cast<int16_t *>(ws + o_bs);
-    uint8_t *bad = ws + o_fl;  // one flag byte per activation block (NaN/Inf present)
-    uint16_t *sj = w->dtype == TRHIP_Q4K ? reinterpret_cast<uint16_t *>(ws + o_sj) : nullptr;  // q4_k msum operands
+        return *status = fail(ctx, TRHIP_ERR_INVALID, std::string(name) + ": shape does not match the store"), 2;
+    if (M == 0 || N == 0) return 1;
+    if (K != 0 && (!x || !c)) return *status = fail(ctx, TRHIP_ERR_INVALID, std::string(name) + ": null x or c"), 2;
+    return 0;
+}
+
+// Quantize x into the scratch `ws` (layout l) and run the integer block kernels.
+int actq_run(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c, int64_t M,
+             int64_t K, int accumulate, uint8_t *ws, const ActqLayout &l) {
+    const int blk = block_elems(w->dtype);
+    int8_t *q = reinterpret_cast<int8_t *>(ws + l.o_q);
+    float *d = reinterpret_cast<float *>(ws + l.o_d);
+    int16_t *bs = reinterpret_cast<int16_t *>(ws + l.o_bs);
+    uint8_t *bad = ws + l.o_fl;  // one flag byte per activation block (NaN/Inf present)
+    uint16_t *sj = w->dtype == TRHIP_Q4K ? reinterpret_cast<uint16_t *>(ws + l.o_sj) : nullptr;  // q4_k msum operands
     const float *xa = x;
-    if (copy_x) {
-        float *tmp = reinterpret_cast<float *>(ws + o_x);
+    if (l.copy_x) {
+        float *tmp = reinterpret_cast<float *>(ws + l.o_x);
         hipError_t e = hipMemcpyAsync(tmp, x, (size_t)(M * K) * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "gemm_q_actq: align x");
         xa = tmp;
     }
-    if ((st = launch_quantize_q8(ctx, xa, M, K, blk, q, d, bs, bad, sj)) != TRHIP_OK) return st;
+    int st = launch_quantize_q8(ctx, xa, M, K, blk, q, d, bs, bad, sj);
+    if (st != TRHIP_OK) return st;
     return launch_actq(ctx, w, row0, N, xa, c, M, accumulate != 0, q, d, bs, bad, sj);
+}
+
+}  // namespace
+
+// The allocation-free act-quant's scratch (trhip_gemm_q_actq_noalloc): one copy per device, held until the process
+// ends. Host code never uses this name as an address: the device address comes from hipGetSymbolAddress, once per
+// device, in trhip_init (scratch_dev below).
+static __device__ __align__(256) uint8_t scratch[TRHIP_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+std::mutex g_scratch_mu;
+void *g_scratch_dev[64] = {};  // device address of `scratch` on device i (set by trhip_init with i current)
+
+// The address of `scratch` on the current device ctx->device; looked up on the first context of a device.
+int scratch_dev(trhip_ctx *ctx) {
+    if (ctx->device < 0 || ctx->device >= 64) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "scratch: device index above 63");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_dev[ctx->device]) {
+        void *ptr = nullptr;
+        hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) return hip_fail(ctx, e != hipSuccess ? e : hipErrorInvalidSymbol, "scratch address");
+        g_scratch_dev[ctx->device] = ptr;
+    }
+    ctx->scratch = static_cast<uint8_t *>(g_scratch_dev[ctx->device]);
+    return TRHIP_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int trhip_gemm_q_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
+                      int64_t M, int64_t K, int accumulate) {
+    if (!ctx || !w) return TRHIP_ERR_INVALID;
+    int st = TRHIP_OK;
+    const int r = actq_check(ctx, w, row0, N, x, c, M, K, "gemm_q_actq", &st);
+    if (r) return st;
+    DevGuard g(ctx);
+    if (K == 0) return accumulate ? TRHIP_OK : zero_f32(ctx, c, M * N);
+    const ActqLayout l = actq_layout(w->dtype, M, K, x);
+    uint8_t *ws = static_cast<uint8_t *>(workspace(ctx, l.total, &st));
+    if (!ws) return st;
+    return actq_run(ctx, w, row0, N, x, c, M, K, accumulate, ws, l);
+}
+
+int trhip_gemm_q_actq_noalloc(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x,
+                              float *c, int64_t M, int64_t K, int accumulate) {
+    if (!ctx || !w) return TRHIP_ERR_INVALID;
+    int st = TRHIP_OK;
+    const int r = actq_check(ctx, w, row0, N, x, c, M, K, "gemm_q_actq_noalloc", &st);
+    if (r) return st;
+    if (K != 0) {
+        const ActqLayout l = actq_layout(w->dtype, M, K, x);
+        if (l.total > (size_t)TRHIP_NOALLOC_SCRATCH_BYTES)
+            return fail(ctx, TRHIP_ERR_INVALID,
+                        "gemm_q_actq_noalloc: M x K needs " + std::to_string(l.total) + " bytes of scratch; the static "
+                        "scratch holds " + std::to_string((size_t)TRHIP_NOALLOC_SCRATCH_BYTES) + " (use trhip_gemm_q_actq)");
+        if (!ctx->scratch) return fail(ctx, TRHIP_ERR_HIP, "gemm_q_actq_noalloc: no scratch address");
+        DevGuard g(ctx);
+        return actq_run(ctx, w, row0, N, x, c, M, K, accumulate, ctx->scratch, l);
+    }
+    DevGuard g(ctx);
+    return accumulate ? TRHIP_OK : zero_f32(ctx, c, M * N);
 }
 
 int trhip_open_q(trhip_ctx *ctx, const trhip_wstore *w, int64_t elem_off, int64_t n, float *out) {

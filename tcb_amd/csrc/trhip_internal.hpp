@@ -206,6 +206,8 @@ struct trhip_ctx {
     int force_exact_rows = 0;   // exact four-lane GEMV rows per workgroup (16, 32, 64)
     int force_exact_lanes = 0;  // exact GEMV lanes per row (4, 8)
     int force_actq_tm = 0;      // act-quant MFMA row tile (32, 64)
+    // Device address of the static scratch array of trhip_gemm_q_actq_noalloc on this context's device.
+    uint8_t *scratch = nullptr;
     int sm_count = 0;
 };
 
