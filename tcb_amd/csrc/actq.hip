@@ -20,7 +20,9 @@
 namespace trhip {
 namespace {
 
-template <int BLK>
+// TILED (blk 256, for the prefill MFMA kernel): codes, scales and msum operands go to the tiled layout of
+// prefill.hip (tiled_q / tiled_d / tiled_sj) instead of row-major, and no 16-sums are written.
+template <int BLK, bool TILED = false>
 __global__ __launch_bounds__(256) void quantize_q8_kernel(const float *__restrict__ x, int64_t M, int64_t K,
                                                           int8_t *__restrict__ q, float *__restrict__ d,
                                                           int16_t *__restrict__ bs, uint8_t *__restrict__ bad_blk,
@@ -67,13 +69,26 @@ __global__ __launch_bounds__(256) void quantize_q8_kernel(const float *__restric
     }
     uint32_t packed = (uint32_t)(c[0] & 0xFF) | ((uint32_t)(c[1] & 0xFF) << 8) | ((uint32_t)(c[2] & 0xFF) << 16) |
                       ((uint32_t)(c[3] & 0xFF) << 24);
-    *reinterpret_cast<uint32_t *>(q + off) = packed;
-    if (l4 == 0) d[blk_id] = dv;
+    const int64_t m = blk_id / nbk, b = blk_id % nbk;
+    if (TILED) {
+        *reinterpret_cast<uint32_t *>(q + tiled_q(m, b, nbk, 4 * l4)) = packed;
+        if (l4 == 0) d[tiled_d(m, b, nbk)] = dv;
+    } else {
+        *reinterpret_cast<uint32_t *>(q + off) = packed;
+        if (l4 == 0) d[blk_id] = dv;
+    }
     int s16 = c[0] + c[1] + c[2] + c[3];
     s16 += __shfl_xor(s16, 1);
     s16 += __shfl_xor(s16, 2);
-    if ((l4 & 3) == 0) bs[off / 16] = (int16_t)s16;
-    if (BLK == 256 && sj) {
+    if (!TILED && (l4 & 3) == 0) bs[off / 16] = (int16_t)s16;
+    if (TILED) {
+        const int s32 = s16 + __shfl_xor(s16, 4);
+        if ((l4 & 7) == 0) {
+            const int j = l4 >> 3, sh = s32 >> 6, sl = s32 & 63;
+            sj[tiled_sj(m, b, nbk, 0, j)] = __builtin_bit_cast(uint16_t, (_Float16)(float)sh);
+            sj[tiled_sj(m, b, nbk, 1, j)] = __builtin_bit_cast(uint16_t, (_Float16)(float)sl);
+        }
+    } else if (BLK == 256 && sj) {
         // 32-element sums S_j = 64*Sh + Sl (Sh = floor(S/64) in [-64, 63], Sl in [0, 63]) as f16 operands of the
         // q4_k prefill kernel's msum product: [Sh_0..Sh_7, Sl_0..Sl_7] per activation block.
         const int s32 = s16 + __shfl_xor(s16, 4);
@@ -209,6 +224,15 @@ int run_valu(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, con
 }
 
 }  // namespace
+
+int launch_quantize_tiles(trhip_ctx *ctx, const float *x, int64_t M, int64_t K, int8_t *qt, float *dt, uint16_t *st,
+                          uint8_t *bad) {
+    if (M == 0 || K == 0) return TRHIP_OK;
+    const int64_t total = M * K / 4;
+    hipLaunchKernelGGL((quantize_q8_kernel<256, true>), dim3((unsigned)((total + 255) / 256)), dim3(256), 0, ctx->stream,
+                       x, M, K, qt, dt, nullptr, bad, st);
+    return launch_check(ctx, "quantize_tiles");
+}
 
 int launch_quantize_q8(trhip_ctx *ctx, const float *x, int64_t M, int64_t K, int blk, int8_t *q, float *d, int16_t *bs,
                        uint8_t *bad, uint16_t *sj) {

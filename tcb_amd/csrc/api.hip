@@ -810,20 +810,23 @@ namespace {
 
 // Scratch layout of the act-quant operator: q [M][K] int8, d [M][K/blk] fp32, bs [M][K/16] int16, one NaN/Inf flag
 // byte per activation block, for q4_k the f16 msum operands [M][K/256][16], and an aligned copy of x when x is not
-// 16-byte aligned.
+// 16-byte aligned. When the q4_k prefill kernel takes the shape (tiles), q, d and the msum operands are in its
+// tiled layout over rows padded to a multiple of 128, and there are no 16-sums.
 struct ActqLayout {
     size_t o_q = 0, o_d = 0, o_bs = 0, o_fl = 0, o_sj = 0, o_x = 0, total = 0;
-    bool copy_x = false;
+    bool copy_x = false, tiles = false;
 };
 
-ActqLayout actq_layout(int dtype, int64_t M, int64_t K, const float *x) {
+ActqLayout actq_layout(int dtype, int64_t M, int64_t N, int64_t row0, int64_t K, const float *x) {
     ActqLayout l;
     const int64_t nb = K / block_elems(dtype);
-    l.o_d = align_up(l.o_q + (size_t)(M * K), 256);
-    l.o_bs = align_up(l.o_d + (size_t)(M * nb) * sizeof(float), 256);
-    l.o_fl = align_up(l.o_bs + (size_t)(M * (K / 16)) * sizeof(int16_t), 256);
+    l.tiles = prefill_tiles_apply(dtype, M, N, row0, K);
+    const int64_t Mq = l.tiles ? (M + kPrefillRowPad - 1) / kPrefillRowPad * kPrefillRowPad : M;
+    l.o_d = align_up(l.o_q + (size_t)(Mq * K), 256);
+    l.o_bs = align_up(l.o_d + (size_t)(Mq * nb) * sizeof(float), 256);
+    l.o_fl = align_up(l.o_bs + (l.tiles ? 0 : (size_t)(M * (K / 16)) * sizeof(int16_t)), 256);
     l.o_sj = align_up(l.o_fl + (size_t)(M * nb), 256);
-    l.o_x = align_up(l.o_sj + (dtype == TRHIP_Q4K ? (size_t)(M * nb) * 32 : 0), 256);
+    l.o_x = align_up(l.o_sj + (dtype == TRHIP_Q4K ? (size_t)(Mq * nb) * 32 : 0), 256);
     l.copy_x = reinterpret_cast<uintptr_t>(x) % 16 != 0;
     l.total = l.o_x + (l.copy_x ? (size_t)(M * K) * sizeof(float) : 0);
     return l;
@@ -857,6 +860,11 @@ int actq_run(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, con
         hipError_t e = hipMemcpyAsync(tmp, x, (size_t)(M * K) * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "gemm_q_actq: align x");
         xa = tmp;
+    }
+    if (l.tiles) {
+        int st = launch_quantize_tiles(ctx, xa, M, K, q, d, sj, bad);
+        if (st != TRHIP_OK) return st;
+        return launch_prefill_q4k(ctx, w, row0, N, xa, c, M, accumulate != 0, q, d, sj, bad);
     }
     int st = launch_quantize_q8(ctx, xa, M, K, blk, q, d, bs, bad, sj);
     if (st != TRHIP_OK) return st;
@@ -899,7 +907,7 @@ int trhip_gemm_q_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64
     if (r) return st;
     DevGuard g(ctx);
     if (K == 0) return accumulate ? TRHIP_OK : zero_f32(ctx, c, M * N);
-    const ActqLayout l = actq_layout(w->dtype, M, K, x);
+    const ActqLayout l = actq_layout(w->dtype, M, N, row0, K, x);
     uint8_t *ws = static_cast<uint8_t *>(workspace(ctx, l.total, &st));
     if (!ws) return st;
     return actq_run(ctx, w, row0, N, x, c, M, K, accumulate, ws, l);
@@ -912,7 +920,7 @@ int trhip_gemm_q_actq_noalloc(trhip_ctx *ctx, const trhip_wstore *w, int64_t row
     const int r = actq_check(ctx, w, row0, N, x, c, M, K, "gemm_q_actq_noalloc", &st);
     if (r) return st;
     if (K != 0) {
-        const ActqLayout l = actq_layout(w->dtype, M, K, x);
+        const ActqLayout l = actq_layout(w->dtype, M, N, row0, K, x);
         if (l.total > (size_t)TRHIP_NOALLOC_SCRATCH_BYTES)
             return fail(ctx, TRHIP_ERR_INVALID,
                         "gemm_q_actq_noalloc: M x K needs " + std::to_string(l.total) + " bytes of scratch; the static "

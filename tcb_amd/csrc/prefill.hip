@@ -1,0 +1,313 @@
+// prefill.hip -- act-quant prefill GEMM for q4_k weights on int8 MFMA, 128 activation rows x 32 weight rows per
+// wave, bit-identical to tensor/cpu_quant_q8.go:91-116 (dotQ4KQ8Go) like actq_mfma_q4k. Taken for grids large
+// enough to fill the device (at least 192 workgroups of 128 x 256).
+//
+// Arithmetic (same as actq_mfma_q4k): per block b and output (m, n), with sc_j = 8 s1 + s0,
+//   isum = sum_i (s0 q4)_i q8_i + 8 sum_i (s1 q4)_i q8_i      two v_mfma_i32_32x32x32_i8 accumulations, exact
+//   msum = sum_j S_j m_j, S_j = 64 Sh_j + Sl_j                 one v_mfma_f32_32x32x16_f16, exact
+//   t = fl(fl(d fl(isum)) - fl(dmin fl(msum)));  acc = fl(acc + fl(t d8))   blocks in order
+//
+// Why this shape. Measured on the device (trhip_mfma_probe and kernels of the same structure): int8 MFMA issues
+// every ~34 cycle units at two waves per SIMD, and independent VALU work hides under it when it is issued between
+// the MFMAs of the same wave (seven VALU per MFMA: ~42 units). A VALU burst after a tile's MFMAs does not hide, and
+// VALU that reads a tile's sums right after its last MFMA stalls the wave for the MFMA latency. The exact epilogue
+// costs seven VALU per output and block, i.e. seven per MFMA of a 32x32 tile. So:
+//   - each wave expands its 32 weight rows' block once (both planes of all eight sub-blocks, 64 registers) and runs
+//     four 32-row activation tiles through it: the expansion's ~135 VALU are spread over 68 MFMAs;
+//   - two accumulator sets are used in turn: while tile t's 16 MFMAs run into one set, the epilogue of tile t - 1
+//     (the previous block's last tile for t = 0) reads the other, two outputs after each MFMA pair;
+//   - weights go to LDS with the activations (global_load_lds, no registers), leaving the registers for the above:
+//     eight waves (256 weight rows) per workgroup, one workgroup per CU, two stages.
+//
+// Staging: the quantizer writes codes, msum operands and scales in the tiled layout (trhip_internal.hpp), so a
+// block's activation data is 9 KB per 32-row tile of 1 KB pieces in operand order, each moved by one
+// global_load_lds_dwordx4; each wave moves its own weight rows' header and codes the same way. One barrier per
+// block: block b + 1 is in flight while block b is computed.
+#include "trhip_internal.hpp"
+#include "mfma_util.hpp"
+
+namespace trhip {
+namespace {
+
+constexpr int PF_W = 8;                 // waves per workgroup, each owning 32 weight rows
+constexpr int PF_TN = 32 * PF_W;        // weight rows per workgroup
+constexpr int PF_THREADS = 64 * PF_W;
+constexpr int PF_MT = 4;                // 32-row activation tiles per wave
+struct Pf {
+    static constexpr int TM = 32 * PF_MT;                   // activation rows per workgroup (and per wave)
+    static constexpr int A = PF_MT * 8192, S = PF_MT * 1024; // codes, msum operands of one block
+    static constexpr int WREG = 512 + 4096;                 // one wave's weight rows: 32 headers, then 32 x 128 codes
+    static constexpr int STAGE = A + S + PF_W * WREG;
+    static constexpr int D = PF_MT * 128;                   // d8 of one block (slot b % 3, read one block later)
+    static constexpr int DOFF = 2 * STAGE;
+    static constexpr size_t LDS = DOFF + 3 * D + (TM + 1) * sizeof(int);
+    static constexpr int PIECES = 9 * PF_MT;                // 1 KB activation pieces per stage
+};
+static_assert(Pf::LDS <= 160 * 1024, "one workgroup per CU");
+
+typedef __attribute__((address_space(3))) void *lds_ptr;
+
+// Raw buffer over [base, base + bytes): per-lane 32-bit offsets, and loads past the end read 0 instead of faulting.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+// SIZE bytes per lane (16 or 4) from rsrc at voffset + soffset + IMM into LDS at l + IMM + SIZE * lane (l
+// wave-uniform; the immediate offset moves the LDS address too, so offsets that differ per piece go in soffset)
+#define BUF_TO_LDS(SIZE, IMM, r, voffset, soffset, l) \
+    __builtin_amdgcn_raw_ptr_buffer_load_lds((r), (lds_ptr)(l), SIZE, (voffset), (soffset), IMM, 0)
+
+// One 32-row tile of a block: 16 int8 MFMAs into (c0, c1), and between them the epilogue of the pending tile held in
+// (p0, p1) with msum pcm, the pending block's d, dmin and the d8 of its rows (pd8, this lane's rows at + 8 (v / 4)
+// + (v % 4)): two outputs after each MFMA pair, in the reference's rounding order.
+__device__ __forceinline__ void pf_tile(v16i &c0, v16i &c1, const v16i &p0, const v16i &p1, const v16f &pcm, float pdd,
+                                        float pdm, float *pacc, const float *pd8, const v4i *ar, const v4i (&b0)[8],
+                                        const v4i (&b1)[8]) {
+    c0 = (v16i){0};
+    c1 = (v16i){0};
+    // LDS reads complete in order, so each is issued a step before it is used and after everything used earlier:
+    // step kc issues d8 of step kc + 1, then A of step kc + 2
+    v4i a[3];
+    a[0] = ar[0];
+    float2 s8n = *reinterpret_cast<const float2 *>(pd8);
+    a[1] = ar[64];
+#pragma unroll
+    for (int kc = 0; kc < 8; kc++) {
+        const float2 s8 = s8n;
+        if (kc + 1 < 8) s8n = *reinterpret_cast<const float2 *>(pd8 + 8 * ((kc + 1) >> 1) + 2 * ((kc + 1) & 1));
+        if (kc + 2 < 8) a[(kc + 2) % 3] = ar[64 * (kc + 2)];
+        c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[kc % 3], b0[kc], c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[kc % 3], b1[kc], c1, 0, 0, 0);
+        const float s8v[2] = {s8.x, s8.y};
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const int v = 2 * kc + r;
+            const int isum = p0[v] + 8 * p1[v];
+            const float tt = (pdd * (float)isum) - (pdm * pcm[v]);
+            pacc[v] = pacc[v] + tt * s8v[r];
+        }
+        // LDS reads first, then each MFMA followed by one output's epilogue
+        const int nreads = (kc + 1 < 8) + (kc + 2 < 8);
+        if (nreads == 2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        else if (nreads == 1) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
+    }
+}
+
+template <bool ACC>
+__global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_q4k(
+    const Planes p, int64_t N, int64_t row0, int64_t M, int64_t K, const float *__restrict__ x,
+    const int8_t *__restrict__ qt, const float *__restrict__ dt, const uint16_t *__restrict__ st,
+    const uint8_t *__restrict__ bad_blk, float *__restrict__ c) {
+    using T = Pf;
+    constexpr int TM = T::TM, STAGE = T::STAGE, MT = PF_MT;
+    extern __shared__ __align__(16) uint8_t lds[];
+    int *rowstate = reinterpret_cast<int *>(lds + T::DOFF + 3 * T::D);  // [TM] 0 ok, 1 NaN/Inf row, 2 outside M
+    int *anybad = rowstate + TM;
+
+    const int nb = (int)p.nb;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int64_t tmi, tni;
+    tile_of(blockIdx.x, (M + TM - 1) / TM, (N + PF_TN - 1) / PF_TN, tmi, tni);
+    const int64_t n0 = tni * PF_TN, m0 = tmi * TM, mt0 = m0 >> 5;
+    tile_row_flags<TM, PF_THREADS>(bad_blk, m0, M, nb, rowstate, anybad);
+
+    // this wave's weight rows: lane l holds row 32 w + l % 32, code bytes 64 (l / 32) + 16 g .. +15 of each block
+    // (elements 16 (l / 32) .. +15 of sub-blocks 2 g (low nibbles) and 2 g + 1 (high nibbles))
+    const int nloc = 32 * w + (lane & 31);
+    // buffers (the launcher checks that every offset fits 32 bits): the tiled activations over rows padded to a
+    // multiple of TM, and the store's rows up to row0 + N
+    const int64_t mpad = (M + TM - 1) / TM * TM;
+    const __amdgpu_buffer_rsrc_t rq = buf_rsrc(qt, (uint32_t)(mpad * nb * 256));
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(st, (uint32_t)(mpad * nb * 32));
+    const __amdgpu_buffer_rsrc_t rd = buf_rsrc(dt, (uint32_t)(mpad * nb * 4));
+    const __amdgpu_buffer_rsrc_t rwq = buf_rsrc(p.qs, (uint32_t)((row0 + N) * nb * 128));
+    const __amdgpu_buffer_rsrc_t rwh = buf_rsrc(p.aux, (uint32_t)((row0 + N) * nb * 16));
+    const uint32_t v16 = 16 * lane;                                                    // activation pieces
+    const uint32_t vd = (uint32_t)((lane >> 5) * nb * 128 + 4 * (lane & 31));         // d8 pieces
+    // weight DMA: codes of 8 rows per instruction, lane j moving 16-byte piece (j % 8) ^ (j / 8) of row j / 8, so
+    // each instruction reads eight whole 128-byte row segments and the LDS slot of piece pc of row r is pc ^ (r % 8)
+    // (conflict-free operand reads); headers by dwords, 16 rows per instruction
+    // (rows past row0 + N read zeros from the buffer's bound; their outputs are not stored)
+    const int jr = lane >> 3, jc = lane & 7;
+    const int64_t wr0 = row0 + n0 + 32 * w;  // this wave's first weight row
+    const uint32_t vq = (uint32_t)((wr0 + jr) * nb * 128 + 16 * (jc ^ jr));   // + 128 b + 8 q nb 128
+    const uint32_t vh = (uint32_t)((wr0 + (lane >> 2)) * nb * 16 + 4 * (lane & 3));  // + 16 b + 16 q nb 16
+
+    // stage block b into buffer buf: 1 KB activation pieces i (i < 8 MT codes of tile i / 8, chunk i % 8, then MT
+    // msum pieces) dealt round-robin to the waves, the d8 pieces (256 bytes, two tiles each) after them, and each
+    // wave's own weight rows
+    auto stage = [&](int b, int buf) {
+        uint8_t *sb = lds + buf * STAGE;
+        uint8_t *db = lds + T::DOFF + (b % 3) * T::D;
+#pragma unroll
+        for (int i = 0; i < T::PIECES; i++) {
+            if (i % PF_W != w) continue;
+            if (i < 8 * MT) {
+                const int t = i >> 3, kc = i & 7;
+                BUF_TO_LDS(16, 0, rq, v16, (uint32_t)((((mt0 + t) * nb + b) * 8 + kc) * 1024), sb + 1024 * i);
+            } else {
+                const int t = i - 8 * MT;
+                BUF_TO_LDS(16, 0, rs, v16, (uint32_t)(((mt0 + t) * nb + b) * 1024), sb + T::A + 1024 * t);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < MT / 2; i++)
+            if ((T::PIECES + i) % PF_W == w)
+                BUF_TO_LDS(4, 0, rd, vd, (uint32_t)(((mt0 + 2 * i) * nb + b) * 128), db + 256 * i);
+        uint8_t *wb = sb + T::A + T::S + w * T::WREG;
+#pragma unroll
+        for (int q = 0; q < 2; q++) BUF_TO_LDS(4, 0, rwh, vh, (uint32_t)(16 * b + 256 * q * nb), wb + 256 * q);
+#pragma unroll
+        for (int q = 0; q < 4; q++) BUF_TO_LDS(16, 0, rwq, vq, (uint32_t)(128 * b + 1024 * q * nb), wb + 512 + 1024 * q);
+    };
+
+    stage(0, 0);
+
+    float accf[MT][16];
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) accf[t][v] = 0.0f;
+    // Pending epilogue state (the tile before the one whose MFMAs run): sums (in set y, or x), msum, d, dmin. Before
+    // the first block nothing is pending: zero sums and msum with zero d8 (slot 2, zeroed here) add +-0 to accf =
+    // +0, which stays +0.
+    v16i x0 = (v16i){0}, x1 = (v16i){0}, y0 = (v16i){0}, y1 = (v16i){0};
+    v16f pcm = (v16f){0.0f};
+    float pdd = 0.0f, pdm = 0.0f;
+    if (tid < T::D / 4) reinterpret_cast<float *>(lds + T::DOFF + 2 * T::D)[tid] = 0.0f;
+    const int lrow = 4 * (lane >> 5);  // this lane's d8 offset within a tile
+
+    for (int b = 0; b < nb; b++) {
+        // this wave's loads of block b have landed; after the barrier everyone's have, and nobody reads the other
+        // buffer (block b - 1) any more
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (b + 1 < nb) stage(b + 1, (b + 1) & 1);
+        const uint8_t *sb = lds + (b & 1) * STAGE;
+
+        // weight block b from LDS: scales and both planes of all eight sub-blocks
+        const uint8_t *wb = sb + T::A + T::S + w * T::WREG;
+        // (addresses recomputed per block from a lane id the compiler cannot hoist: no registers held across blocks)
+        const int ln = (int)opaque((uint32_t)lane), r = ln & 31, h = ln >> 5;
+        const uint4 wh = *reinterpret_cast<const uint4 *>(wb + 16 * r);
+        uint4 wq[4];  // pieces 4 h + g of row r
+        const uint8_t *wrb = wb + 512 + 1024 * (r >> 3) + 128 * (r & 7);
+#pragma unroll
+        for (int g = 0; g < 4; g++) wq[g] = *reinterpret_cast<const uint4 *>(wrb + 16 * ((4 * h + g) ^ (r & 7)));
+        uint32_t sc_lo, sc_hi, m_lo, m_hi;
+        q4k_scales(wh.y, wh.z, wh.w, sc_lo, sc_hi, m_lo, m_hi);
+        const float dd = f16_to_f32((uint16_t)(wh.x & 0xFFFF)), dm = f16_to_f32((uint16_t)(wh.x >> 16));
+        v4i b0[8], b1[8];
+#pragma unroll
+        for (int kc = 0; kc < 8; kc++) {
+            const uint4 raw = wq[kc >> 1];
+            const uint4 nib = (kc & 1) ? make_uint4((raw.x >> 4) & 0x0F0F0F0Fu, (raw.y >> 4) & 0x0F0F0F0Fu,
+                                                    (raw.z >> 4) & 0x0F0F0F0Fu, (raw.w >> 4) & 0x0F0F0F0Fu)
+                                       : make_uint4(raw.x & 0x0F0F0F0Fu, raw.y & 0x0F0F0F0Fu, raw.z & 0x0F0F0F0Fu,
+                                                    raw.w & 0x0F0F0F0Fu);
+            const uint32_t sc = ((kc < 4 ? sc_lo : sc_hi) >> (8 * (kc & 3))) & 0xFF;
+            b0[kc] = mul16(nib, sc & 7);
+            b1[kc] = mul16(nib, sc >> 3);
+        }
+        // msum B operand of this lane's row: [64 m_0..7 | m_0..7] (lanes < 32 hold k 0..7, lanes >= 32 k 8..15)
+        const uint32_t mul = (lane >> 5) ? 1u : 64u;
+        const v8h bmv = __builtin_bit_cast(
+            v8h, make_uint4(pack_h2(mul * (m_lo & 0xFF), mul * ((m_lo >> 8) & 0xFF)),
+                            pack_h2(mul * ((m_lo >> 16) & 0xFF), mul * (m_lo >> 24)),
+                            pack_h2(mul * (m_hi & 0xFF), mul * ((m_hi >> 8) & 0xFF)),
+                            pack_h2(mul * ((m_hi >> 16) & 0xFF), mul * (m_hi >> 24))));
+
+        const v4i *ar = reinterpret_cast<const v4i *>(sb) + lane;  // tile t, chunk kc: + 512 t + 64 kc
+        const v8h *am = reinterpret_cast<const v8h *>(sb + T::A) + lane;  // tile t: + 64 t
+        const float *d8b = reinterpret_cast<const float *>(lds + T::DOFF + (b % 3) * T::D) + lrow;
+        const float *d8p = reinterpret_cast<const float *>(lds + T::DOFF + ((b + 2) % 3) * T::D) + lrow;
+        // tiles 0..3 in sets x, y, x, y; each one's epilogue runs inside the next tile
+        pf_tile(x0, x1, y0, y1, pcm, pdd, pdm, accf[MT - 1], d8p + 32 * (MT - 1), ar, b0, b1);
+        pcm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[0], bmv, (v16f){0.0f}, 0, 0, 0);
+        pdd = dd;
+        pdm = dm;
+        pf_tile(y0, y1, x0, x1, pcm, pdd, pdm, accf[0], d8b, ar + 512, b0, b1);
+        pcm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[64], bmv, (v16f){0.0f}, 0, 0, 0);
+        pf_tile(x0, x1, y0, y1, pcm, pdd, pdm, accf[1], d8b + 32, ar + 1024, b0, b1);
+        pcm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[128], bmv, (v16f){0.0f}, 0, 0, 0);
+        pf_tile(y0, y1, x0, x1, pcm, pdd, pdm, accf[2], d8b + 64, ar + 1536, b0, b1);
+        pcm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[192], bmv, (v16f){0.0f}, 0, 0, 0);
+    }
+    {  // the last block's last tile (set y)
+        const float *d8l = reinterpret_cast<const float *>(lds + T::DOFF + ((nb + 2) % 3) * T::D) + lrow + 32 * (MT - 1);
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int isum = y0[v] + 8 * y1[v];
+            const float tt = (pdd * (float)isum) - (pdm * pcm[v]);
+            accf[MT - 1][v] = accf[MT - 1][v] + tt * d8l[8 * (v >> 2) + (v & 3)];
+        }
+    }
+
+    const int64_t gn = n0 + nloc;
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int mloc = 32 * t + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+            if (gn < N && rowstate[mloc] == 0) {
+                float *o = c + (m0 + mloc) * N + gn;
+                *o = ACC ? *o + accf[t][v] : accf[t][v];
+            }
+        }
+    }
+    // rows holding NaN/Inf take the exact fp32 path (quantGemv) on their own; rare
+    if (!*anybad) return;
+    for (int i = tid; i < TM * PF_TN; i += PF_THREADS) {
+        const int ml = i / PF_TN, nl = i % PF_TN;
+        const int64_t gn2 = n0 + nl;
+        if (rowstate[ml] != 1 || gn2 >= N) continue;
+        const int64_t gm = m0 + ml;
+        const float v = exact_dot_row<kQ4K>(p, row0 + gn2, x + gm * K, K);
+        float *o = c + gm * N + gn2;
+        *o = ACC ? *o + v : v;
+    }
+}
+
+}  // namespace
+
+// Taken when the grid of 128 x 256 tiles has at least 192 workgroups (one per CU fits), else the 64-row kernel of
+// actq_mfma.hip keeps more of the device busy.
+namespace {
+// every buffer offset of the kernel fits 32 bits (tiled activations, the store's rows up to row0 + N)
+bool prefill_fits32(int64_t M, int64_t N, int64_t row0, int64_t K) {
+    const int64_t mpad = (M + Pf::TM - 1) / Pf::TM * Pf::TM, nb = K / 256;
+    return mpad * nb * 256 < ((int64_t)1 << 32) && (row0 + N + PF_TN) * nb * 128 < ((int64_t)1 << 32);
+}
+}  // namespace
+
+bool prefill_tiles_apply(int dtype, int64_t M, int64_t N, int64_t row0, int64_t K) {
+    if (dtype != kQ4K || !prefill_fits32(M, N, row0, K)) return false;
+    const int64_t wgs = ((M + Pf::TM - 1) / Pf::TM) * ((N + PF_TN - 1) / PF_TN);
+    return M >= 256 && wgs >= 192;
+}
+
+int launch_prefill_q4k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
+                       int64_t M, bool acc, const int8_t *qt, const float *dt, const uint16_t *st, const uint8_t *bad) {
+    using T = Pf;
+    static_assert(T::TM == kPrefillRowPad, "the tiled layout pads rows to one workgroup row tile");
+    const int64_t wgs = ((M + T::TM - 1) / T::TM) * ((N + PF_TN - 1) / PF_TN);
+    if (wgs >= ((int64_t)1 << 31)) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "prefill: grid too large");
+    if (!prefill_fits32(M, N, row0, w->K)) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "prefill: buffers above 4 GB");
+    const void *fn = acc ? reinterpret_cast<const void *>(&prefill_q4k<true>)
+                         : reinterpret_cast<const void *>(&prefill_q4k<false>);
+    int st0 = allow_dyn_lds(ctx, fn, T::LDS, "prefill: LDS size");
+    if (st0 != TRHIP_OK) return st0;
+    if (acc)
+        hipLaunchKernelGGL((prefill_q4k<true>), dim3((unsigned)wgs), dim3(PF_THREADS), T::LDS, ctx->stream,
+                           w->planes(), N, row0, M, w->K, x, qt, dt, st, bad, c);
+    else
+        hipLaunchKernelGGL((prefill_q4k<false>), dim3((unsigned)wgs), dim3(PF_THREADS), T::LDS, ctx->stream,
+                           w->planes(), N, row0, M, w->K, x, qt, dt, st, bad, c);
+    return launch_check(ctx, "prefill_q4k");
+}
+
+}  // namespace trhip

@@ -169,6 +169,21 @@ __device__ __forceinline__ float exact_dot_row(const Planes p, int64_t row, cons
     return (s0 + s2) + (s1 + s3);
 }
 
+// Tiled activation layout of the q4_k prefill kernel (prefill.hip), per 32-row tile mt = m / 32 and block b, in
+// the operand order of its MFMAs so that each 1 KB piece is one coalesced load straight into LDS:
+//   codes   : 8 KB = chunk kc (32 elements of sub-block kc) x lane (r + 32 h) x 16 bytes (elements 32 kc + 16 h + i)
+//   msum    : 1 KB = lane (r + 32 half) x 8 f16: half 0 = Sh_0..7, half 1 = Sl_0..7 (S_j = 64 Sh_j + Sl_j)
+//   scales  : 32 floats d8 of rows r
+// Rows are padded to a multiple of 128 (a workgroup's row tile); pad rows hold no meaningful values.
+__host__ __device__ inline int64_t tiled_q(int64_t m, int64_t b, int64_t nb, int k) {
+    return (((m >> 5) * nb + b) * 8 + (k >> 5)) * 1024 + ((m & 31) + 32 * ((k >> 4) & 1)) * 16 + (k & 15);
+}
+__host__ __device__ inline int64_t tiled_d(int64_t m, int64_t b, int64_t nb) { return ((m >> 5) * nb + b) * 32 + (m & 31); }
+__host__ __device__ inline int64_t tiled_sj(int64_t m, int64_t b, int64_t nb, int half, int j) {  // in f16 units
+    return ((m >> 5) * nb + b) * 512 + ((m & 31) + 32 * half) * 8 + j;
+}
+constexpr int64_t kPrefillRowPad = 128;
+
 }  // namespace trhip
 
 
@@ -258,6 +273,12 @@ int launch_gemm_rows_fast(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, i
 int launch_quantize_q8(trhip_ctx *ctx, const float *x, int64_t M, int64_t K, int blk, int8_t *q, float *d,
                        int16_t *bs, uint8_t *bad, uint16_t *sj);
 int launch_read_probe(trhip_ctx *ctx, const void *p, int64_t bytes);
+// The q4_k prefill path over the tiled activation layout: whether it takes (M, N), the tiled quantizer, the kernel.
+bool prefill_tiles_apply(int dtype, int64_t M, int64_t N, int64_t row0, int64_t K);
+int launch_quantize_tiles(trhip_ctx *ctx, const float *x, int64_t M, int64_t K, int8_t *qt, float *dt, uint16_t *st,
+                          uint8_t *bad);
+int launch_prefill_q4k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
+                       int64_t M, bool acc, const int8_t *qt, const float *dt, const uint16_t *st, const uint8_t *bad);
 int launch_mfma_probe(trhip_ctx *ctx, int valu_per_mfma, int waves_per_simd, int64_t iters);
 int launch_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                 int64_t M, bool acc, const int8_t *q, const float *d, const int16_t *bs, const uint8_t *bad,

@@ -395,6 +395,32 @@ def test_actq_tiles_bits(backend, M, N, K, row0, acc):
     w.release()
 
 
+@pytest.mark.parametrize("M,N,K,row0,acc,x_off", [(300, 16421, 512, 5, True, 0), (257, 49153, 256, 0, False, 4),
+                                                  (384, 12800, 1024, 0, True, 0)])
+def test_prefill_tiles_bits(backend, M, N, K, row0, acc, x_off):
+    """The 128-row-per-wave prefill kernel (taken for grids of at least 384 128x128 tiles): rows padded past M,
+    ragged N, a row slice of the store, both accumulate modes, an unaligned x, x1000 / zero / +-1 rows and a NaN row
+    (its outputs from the fp32 path): bit-identical to the oracle."""
+    rng = _rng(M + N + K)
+    raw = _weights(Q4K, row0 + N, K, M * 3 + K)
+    X = _x(rng, M * K).reshape(M, K)
+    X[1] *= 1000
+    X[2, :256] = 0
+    X[3] = 1 - 2 * (np.arange(K) % 2)
+    X[M - 2, 11] = np.nan
+    w = backend.FromQuantized(Q4K, raw, row0 + N, K)
+    c0 = _x(rng, M * N) if acc else np.zeros(M * N, np.float32)
+    xb = backend.ctx.alloc(M * K * 4 + 16)
+    xb.upload(X, byte_offset=x_off)
+    cb = backend.ctx.to_device(c0)
+    backend.GemmActQuant(M, N, K, (xb, x_off), w, cb, row0=row0, accumulate=acc)
+    rows = np.ascontiguousarray(raw.reshape(row0 + N, -1)[row0:])
+    same_bits(cb.download(np.float32, M * N), O.quant_gemm_act(Q4K, M, N, K, X, rows, c0))
+    for b in (xb, cb):
+        b.free()
+    w.release()
+
+
 @pytest.mark.parametrize("dt,N,K,M", [(Q4, 14336, 4096, 8), (Q4, 4096, 14336, 8), (Q4K, 4096, 4096, 16),
                                       (Q6K, 1024, 4096, 16)])
 def test_gemm_rows_llama_shapes_bits(backend, dt, N, K, M):

@@ -1,7 +1,7 @@
 """The allocation-free act-quant entry point (trhip_gemm_q_actq_noalloc, static device scratch) through the C-ABI:
-the same bits as trhip_gemm_q_actq on two calls in a row (the second smaller, so the scratch holds the first call's
-contents), in set and accumulate mode, with an unaligned activation pointer and a NaN row, and sizes beyond the
-scratch refused before anything runs."""
+the same bits as trhip_gemm_q_actq on calls in a row, each smaller than the one before (so the scratch holds the last
+call's contents; one q4_k call takes the tiled 128-row prefill kernel), in set and accumulate mode, with an unaligned
+activation pointer and a NaN row, and sizes beyond the scratch refused before anything runs."""
 import numpy as np
 import pytest
 
@@ -11,7 +11,7 @@ from tcb_amd import Q4, Q4K, Q6K, _lib, synth
 
 pytestmark = pytest.mark.gpu
 
-CASES = {Q4K: [(512, 4096, 4096), (40, 300, 2048)], Q4: [(96, 1024, 4096), (9, 130, 1024)],
+CASES = {Q4K: [(512, 4096, 4096), (256, 24576, 1024), (40, 300, 2048)], Q4: [(96, 1024, 4096), (9, 130, 1024)],
          Q6K: [(64, 1024, 4096), (5, 77, 2048)]}
 
 
