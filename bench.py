@@ -15,11 +15,12 @@ restatement of the reference's sdotq4k path (oracle/trq_avx2.c), all host cores,
 
 Prints one JSON line. --gpus N > 1 exits: the measurement covers one GPU.
 
---profile-kernel {gemv,prefill,rows,copy,read,open_q} runs only that kernel, eagerly, --steps times (for rocprofv3
-runs): gemv = the headline GEMV over the cold ring, prefill = one act-quant GEMM per step, rows = one M > 1 fp32 GEMM
-(--rows-m rows, --rows-shape dtype,N,K, --mode exact or fast) per step, copy = a plain device copy of COPY_BYTES
-(torch) that calibrates the FETCH_SIZE / WRITE_SIZE counters, read = the streaming-read probe over a cold ring of the
-headline's bytes, open_q = OpenQuant of the headline store.
+--profile-kernel {gemv,prefill,rows,copy,read,open_q,sweep,mfma} runs only that work, eagerly, --steps times (for
+rocprofv3 runs): gemv = the headline GEMV over the cold ring, prefill = one act-quant GEMM per step, rows = one M > 1
+fp32 GEMM (--rows-m rows, --rows-shape dtype,N,K, --mode exact or fast) per step, copy = a plain device copy of
+COPY_BYTES (torch) that calibrates the FETCH_SIZE / WRITE_SIZE counters, read = the streaming-read probe over a cold
+ring of the headline's bytes, open_q = OpenQuant of the headline store, sweep = the 32-layer decode sweep (--rows-m
+batch, --mode) launched eagerly, mfma = the int8 matrix-core probe without and with VALU beside it.
 """
 import argparse
 import json
@@ -34,6 +35,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "Q4_K GEMV µs + HBM GB/s (% peak) at 8B shapes; prefill GEMM int8 TOPS"
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, datasheet
+Q4K_CODE = 3
 INT8_PEAK_TOPS = 5033.0      # MI355X dense int8 MFMA, datasheet (5.03 POPS)
 N, K = 14336, 4096
 RING_BYTES = int(1.1 * (1 << 30))
@@ -64,7 +66,8 @@ def parse():
     ap.add_argument("--sweep", type=int, default=1, help="also time the 32-layer decode sweep (0 = skip)")
     ap.add_argument("--shapes", type=int, default=1,
                     help="also time every Llama-3-8B GEMV shape per dtype and the prefill grid (0 = skip)")
-    ap.add_argument("--profile-kernel", choices=["gemv", "prefill", "rows", "copy", "read", "open_q"], default=None,
+    ap.add_argument("--profile-kernel", choices=["gemv", "prefill", "rows", "copy", "read", "open_q", "sweep", "mfma"],
+                    default=None,
                     help="run only this kernel --steps times, eagerly (counter runs)")
     ap.add_argument("--rows-m", type=int, default=16, help="activation rows of --profile-kernel rows (M > 1 path)")
     ap.add_argument("--rows-shape", default="q4_k,14336,4096",
@@ -279,6 +282,32 @@ def profile_kernel(a):
         print(json.dumps({"profiled": "copy", "launches": a.steps, "bytes_read": COPY_BYTES, "bytes_written": COPY_BYTES}))
         return 0
     tb = QuantBackend(0)
+    if a.profile_kernel == "mfma":
+        for v in (0, 6, 8):
+            _ = mfma_rate(tb, v, 2)
+        print(json.dumps({"profiled": "mfma_probe", "valu_per_mfma": [0, 6, 8], "waves_per_simd": 2}))
+        tb.close()
+        return 0
+    if a.profile_kernel == "sweep":
+        # every linear of the 32-layer sweep and the head, launched eagerly (no graph), --steps token steps
+        from tcb_amd import Q6K
+        b = a.rows_m
+        mode = MODE_FAST if a.mode == "fast" else MODE_EXACT
+        host = {name: synth.random_blocks(Q4K, n, k, seed=10 + i) for i, (name, n, k) in enumerate(LAYER)}
+        stores = [[tb.FromQuantized(Q4K, host[name], n, k) for name, n, k in LAYER] for _ in range(N_LAYERS)]
+        head = tb.FromQuantized(Q6K, synth.random_blocks(Q6K, VOCAB, HIDDEN, seed=99), VOCAB, HIDDEN)
+        xs = {4096: tb.ctx.to_device(synth.activations(b, 4096, seed=7)),
+              14336: tb.ctx.to_device(synth.activations(b, 14336, seed=8))}
+        cb = tb.ctx.alloc(b * VOCAB * 4)
+        for _ in range(a.steps):
+            for layer in stores:
+                for (name, n, k), w in zip(LAYER, layer):
+                    tb.GemmSet(b, n, k, xs[k], w, cb, mode=mode)
+            tb.GemmSet(b, VOCAB, HIDDEN, xs[4096], head, cb, mode=mode)
+        tb.ctx.sync()
+        print(json.dumps({"profiled": "decode_sweep_eager", "batch": b, "mode": a.mode, "token_steps": a.steps}))
+        tb.close()
+        return 0
     raw = synth.quant_weights(Q4K, N, K, seed=3, outliers=0.01)
     if a.profile_kernel == "gemv":
         ring = [tb.FromQuantized(Q4K, raw, N, K) for _ in range(max(2, -(-RING_BYTES // raw.nbytes)))]
@@ -337,6 +366,48 @@ def profile_kernel(a):
         print(json.dumps({"profiled": "prefill_q4_k_M%d" % M, "launches": a.steps, "ops": 2 * M * N * K}))
     tb.close()
     return 0
+
+
+def mfma_rate(tb, valu_per_mfma, waves_per_simd, iters=40000):
+    """int8 TOPS of trhip_mfma_probe: four independent v_mfma_i32_32x32x32_i8 chains per wave with valu_per_mfma
+    independent fp32 FMAs beside each MFMA, one workgroup per CU."""
+    from tcb_amd import _lib
+    L = _lib.lib()
+    ctx = tb.ctx
+    L.trhip_mfma_probe(ctx.h, valu_per_mfma, waves_per_simd, 100)
+    ctx.sync()
+    e0, e1 = ctx.event(), ctx.event()
+    ctx.record(e0)
+    rc = L.trhip_mfma_probe(ctx.h, valu_per_mfma, waves_per_simd, iters)
+    ctx.record(e1)
+    if rc:
+        raise RuntimeError("mfma probe failed: %d" % rc)
+    ms = ctx.elapsed_ms(e0, e1)
+    cus = 256
+    return 4.0 * waves_per_simd * cus * iters * 4 * 65536 / (ms * 1e-3) / 1e12
+
+
+def upload_rates(tb, raw):
+    """Store creation (upload + repack) of the headline weights: GB/s of GGUF bytes from pageable host memory and
+    from a trhip_host_alloc (pinned) block, median of 5."""
+    import numpy as np
+    ctx = tb.ctx
+    out = {}
+    pinned, p = ctx.host_alloc(raw.nbytes)
+    pinned[:] = raw
+    for name, src in (("pageable", raw), ("pinned", pinned)):
+        ts = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            w = tb.FromQuantized(Q4K_CODE, src, N, K)  # returns after the upload and repack completed (sync)
+            ts.append(time.perf_counter() - t0)
+            w.release()
+        t = sorted(ts)[len(ts) // 2]
+        out[name] = {"ms": round(t * 1e3, 2), "GB/s": round(raw.nbytes / t / 1e9, 2)}
+    ctx.host_free(p)
+    out["workload"] = "trhip_wstore_create of q4_k %dx%d (%d B), host to device through the upload ring + repack" % (
+        N, K, raw.nbytes)
+    return out
 
 
 def time_graph(tb, graph, replays):
@@ -453,13 +524,19 @@ def main():
         ms = time_graph(tb, gp, reps) / reps
         L.trhip_graph_destroy(gp)
         tops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+        ceiling = mfma_rate(tb, 0, 2)
+        ceiling7 = mfma_rate(tb, 6, 2)
         prefill = {"workload": "act-quant GEMM q4_k %dx%d, M=%d (quantize + int block sums + fp32 epilogue)" % (N, K, M),
                    "us": round(ms * 1e3, 2), "int8_tops": round(tops, 2),
                    "frac_of_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                   "measured_int8_mfma_tops": round(ceiling, 1),
+                   "measured_int8_mfma_tops_6valu": round(ceiling7, 1),
+                   "frac_of_measured_int8": round(tops / ceiling, 4),
                    "traffic_bytes": PREFILL_TRAFFIC if M == 512 else None}
         Xb.free()
         Cb.free()
 
+    upload = upload_rates(tb, raw)
     sweep = decode_sweep(tb, (1, 16), mode) if a.sweep else None
     shapes = shape_table(tb) if a.shapes else None
 
@@ -520,6 +597,7 @@ def main():
                      "frac": round(gbs_cold / HBM_PEAK_GBS, 4), "traffic": TRAFFIC.get(a.mode),
                      "kernel": "gemv_q4_k_%s" % a.mode, "algorithmic_bytes_per_launch": abytes},
         "prefill": prefill,
+        "store_upload": upload,
         "decode_sweep": sweep,
         "shapes": shapes,
         "cpu_baseline": cpu,
