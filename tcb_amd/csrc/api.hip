@@ -200,9 +200,21 @@ int trhip_init(int device, trhip_ctx **out) {
     }
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, device) == hipSuccess) ctx->sm_count = prop.multiProcessorCount;
-    const int st = scratch_dev(ctx);
+    int st = scratch_dev(ctx);
+    if (st == TRHIP_OK) {  // arrival counters start at zero; every kernel that counts leaves them at zero
+        const size_t ab = (size_t)trhip_ctx::kArrivalSlots * sizeof(uint32_t);
+        e = hipMalloc(reinterpret_cast<void **>(&ctx->arrivals), ab);
+        if (e != hipSuccess) {
+            ctx->arrivals = nullptr;
+            st = hip_fail(ctx, e, "init: arrival counters");
+        } else if ((st = zero_f32(ctx, reinterpret_cast<float *>(ctx->arrivals), trhip_ctx::kArrivalSlots)) == TRHIP_OK &&
+                   (e = hipStreamSynchronize(ctx->stream)) != hipSuccess) {
+            st = hip_fail(ctx, e, "init: arrival counters");
+        }
+    }
     if (st != TRHIP_OK) {
         g_noctx_err = ctx->err;
+        if (ctx->arrivals) (void)hipFree(ctx->arrivals);
         (void)hipStreamDestroy(ctx->stream);
         delete ctx;
         return st;
@@ -217,6 +229,7 @@ int trhip_destroy(trhip_ctx *ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->ws) (void)hipFree(ctx->ws);
     if (ctx->ws2) (void)hipFree(ctx->ws2);
+    if (ctx->arrivals) (void)hipFree(ctx->arrivals);
     for (void *p : ctx->retired) (void)hipFree(p);
     if (ctx->idx_host) (void)hipHostFree(ctx->idx_host);
     if (ctx->idx_done) (void)hipEventDestroy(ctx->idx_done);
@@ -415,6 +428,11 @@ int trhip_set_launch_shape(trhip_ctx *ctx, int knob, int a, int b, int c, int d)
         if (!(reset || ((a == 32 || a == 64) && !b && !c && !d)))
             return fail(ctx, TRHIP_ERR_INVALID, "set_launch_shape: act-quant row tile must be 32 or 64");
         ctx->force_actq_tm = a;
+        return TRHIP_OK;
+    case TRHIP_KNOB_ROWS16:
+        if (!(reset || ((a == 1 || a == 2) && b >= 1 && b <= 64 && !c && !d)))
+            return fail(ctx, TRHIP_ERR_INVALID, "set_launch_shape: rows16 takes 1 or 2 tiles per wave and 1..64 slices");
+        ctx->force_rows16 = reset ? 0 : 100 * a + b;
         return TRHIP_OK;
     }
     return fail(ctx, TRHIP_ERR_INVALID, "set_launch_shape: unknown knob");
@@ -751,8 +769,13 @@ int trhip_gemm_q(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N,
         }
         return launch_gemv(ctx, w, row0, N, xa, c, accumulate != 0, mode);
     }
-    // fast mode (tolerance) on matrix cores over fixed-point activations: q4_k from M = 5 (up to 4 rows the exact
-    // kernel's 4-row tiles are as fast), q6_k from M = 2; q8_0 / q4_0 run exact (their fast kernel measured slower)
+    // fast mode (tolerance) on matrix cores: q4_k from M = 5 (up to 4 rows the exact kernel's 4-row tiles are as
+    // fast), up to 16 rows in one launch over f16 activation pairs, more over fixed-point digits; q6_k from M = 2;
+    // q8_0 / q4_0 run exact (their fast kernel measured slower)
+    if (mode == TRHIP_MODE_FAST && w->dtype == TRHIP_Q4K && M > 4 && M <= 16) {
+        const int r = launch_rows16_q4k(ctx, w, row0, N, x, c, M, accumulate != 0);
+        if (r != -1) return r;
+    }
     if (mode == TRHIP_MODE_FAST && ((w->dtype == TRHIP_Q4K && M > 4) || (w->dtype == TRHIP_Q6K && M > 1)))
         return launch_gemm_rows_fast(ctx, w, row0, N, x, c, M, accumulate != 0);
     return launch_gemm_rows(ctx, w, row0, N, x, c, M, accumulate != 0);
@@ -786,6 +809,10 @@ int trhip_gemm_q_swiglu(trhip_ctx *ctx, const trhip_wstore *w, const float *x, f
     float *gu = static_cast<float *>(workspace2(ctx, (size_t)(M * w->N) * sizeof(float), &st));
     if (!gu) return st;
     // fast M > 1 on matrix cores (as trhip_gemm_q dispatches it): the gate fused into the K-slice sum
+    if (mode == TRHIP_MODE_FAST && K > 0 && w->dtype == TRHIP_Q4K && M > 4 && M <= 16) {
+        const int r = launch_rows16_q4k(ctx, w, 0, w->N, x, nullptr, M, false, out);
+        if (r != -1) return r;
+    }
     if (mode == TRHIP_MODE_FAST && K > 0 && ((w->dtype == TRHIP_Q4K && M > 4) || (w->dtype == TRHIP_Q6K && M > 1)))
         return launch_gemm_rows_fast(ctx, w, 0, w->N, x, gu, M, false, out);
     if ((st = trhip_gemm_q(ctx, w, 0, w->N, x, gu, M, K, 0, mode)) != TRHIP_OK) return st;

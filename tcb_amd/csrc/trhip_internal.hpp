@@ -152,21 +152,26 @@ __device__ __forceinline__ float silu_ref(float x) {
     return (s == 0.0f ? 0.0f : x) * s;
 }
 
-// Exact fp32 dot of activation row xr with weight row `row` in sdot32 order (fallback for rows with
-// NaN/Inf; one thread, 32 chains).
+// Exact fp32 dot of activation row xr with weight row `row` over elements [k0, k1) (multiples of 32) in sdot32
+// order (fallback for rows with NaN/Inf; one thread, 32 chains).
 template <int DT>
-__device__ __forceinline__ float exact_dot_row(const Planes p, int64_t row, const float *__restrict__ xr, int64_t K) {
+__device__ __forceinline__ float exact_dot_range(const Planes p, int64_t row, const float *__restrict__ xr, int64_t k0,
+                                                 int64_t k1) {
     float acc[32];
 #pragma unroll
     for (int l = 0; l < 32; l++) acc[l] = 0.0f;
-    for (int64_t k0 = 0; k0 < K; k0 += 32)
+    for (int64_t k = k0; k < k1; k += 32)
 #pragma unroll
-        for (int l = 0; l < 32; l++) acc[l] = fmaf(xr[k0 + l], deq_at<DT>(p, row, k0 + l), acc[l]);
+        for (int l = 0; l < 32; l++) acc[l] = fmaf(xr[k + l], deq_at<DT>(p, row, k + l), acc[l]);
     float Y[8];
 #pragma unroll
     for (int l = 0; l < 8; l++) Y[l] = (acc[l] + acc[8 + l]) + (acc[16 + l] + acc[24 + l]);
     float s0 = Y[0] + Y[4], s1 = Y[1] + Y[5], s2 = Y[2] + Y[6], s3 = Y[3] + Y[7];
     return (s0 + s2) + (s1 + s3);
+}
+template <int DT>
+__device__ __forceinline__ float exact_dot_row(const Planes p, int64_t row, const float *__restrict__ xr, int64_t K) {
+    return exact_dot_range<DT>(p, row, xr, 0, K);
 }
 
 // Tiled activation layout of the q4_k prefill kernel (prefill.hip), per 32-row tile mt = m / 32 and block b, in
@@ -221,6 +226,11 @@ struct trhip_ctx {
     int force_exact_rows = 0;   // exact four-lane GEMV rows per workgroup (16, 32, 64)
     int force_exact_lanes = 0;  // exact GEMV lanes per row (4, 8)
     int force_actq_tm = 0;      // act-quant MFMA row tile (32, 64)
+    int force_rows16 = 0;       // batched-decode q4_k kernel: 100 tiles per wave + K slices
+    // Arrival counters of kernels whose K slices are summed by the workgroup that finishes a row tile last
+    // (rows16.hip): kArrivalSlots zeroed words, each returned to zero by that workgroup.
+    static constexpr int64_t kArrivalSlots = 65536;
+    uint32_t *arrivals = nullptr;
     // Device address of the static scratch array of trhip_gemm_q_actq_noalloc on this context's device.
     uint8_t *scratch = nullptr;
     int sm_count = 0;
@@ -280,6 +290,10 @@ int launch_quantize_tiles(trhip_ctx *ctx, const float *x, int64_t M, int64_t K, 
 int launch_prefill_q4k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                        int64_t M, bool acc, const int8_t *qt, const float *dt, const uint16_t *st, const uint8_t *bad);
 int launch_mfma_probe(trhip_ctx *ctx, int valu_per_mfma, int waves_per_simd, int64_t iters);
+// Fast-mode q4_k product for 1 <= M <= 16 activation rows in one launch (rows16.hip); swi as in
+// launch_gemm_rows_fast. Returns -1 (nothing launched) where it does not apply.
+int launch_rows16_q4k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
+                      int64_t M, bool acc, float *swi = nullptr);
 int launch_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                 int64_t M, bool acc, const int8_t *q, const float *d, const int16_t *bs, const uint8_t *bad,
                 const uint16_t *sj);
