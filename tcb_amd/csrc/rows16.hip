@@ -81,14 +81,15 @@ __device__ __forceinline__ void r16_consts(R16K &k, const R16W &r, int g) {
 
 // The 8 operand halves of step s (qs dword s of the pair: bytes 32g + 4s .. + 3) as exact q sc, in the order
 // (byte 0, 2, 1, 3) low nibbles, then the same bytes' high nibbles; the activation planes use the same order.
-__device__ __forceinline__ v8h r16_codes(const R16W &r, const R16K &k, int s) {
+// (k6464 = 0x64006400 in a register: with the mask as the one literal, each pair is one v_and_or_b32)
+__device__ __forceinline__ v8h r16_codes(const R16W &r, const R16K &k, int s, uint32_t k6464) {
     const uint32_t wd = s == 0 ? r.a.x : s == 1 ? r.a.y : s == 2 ? r.a.z : s == 3 ? r.a.w
                       : s == 4 ? r.b.x : s == 5 ? r.b.y : s == 6 ? r.b.z : r.b.w;
     const uint32_t w8 = wd >> 8;
-    const h2 p0 = __builtin_bit_cast(h2, (wd & 0x000F000Fu) | 0x64006400u);
-    const h2 p1 = __builtin_bit_cast(h2, (wd & 0x00F000F0u) | 0x64006400u);
-    const h2 p2 = __builtin_bit_cast(h2, (w8 & 0x000F000Fu) | 0x64006400u);
-    const h2 p3 = __builtin_bit_cast(h2, (w8 & 0x00F000F0u) | 0x64006400u);
+    const h2 p0 = __builtin_bit_cast(h2, (wd & 0x000F000Fu) | k6464);
+    const h2 p1 = __builtin_bit_cast(h2, (wd & 0x00F000F0u) | k6464);
+    const h2 p2 = __builtin_bit_cast(h2, (w8 & 0x000F000Fu) | k6464);
+    const h2 p3 = __builtin_bit_cast(h2, (w8 & 0x00F000F0u) | k6464);
     const h2 ml = (h2){k.mul.x, k.mul.x}, ol = (h2){k.off.x, k.off.x};
     const h2 mh = (h2){k.mul.y, k.mul.y}, oh = (h2){k.off.y, k.off.y};
     const h2 q0 = __builtin_elementwise_fma(p0, ml, ol), q2 = __builtin_elementwise_fma(p2, ml, ol);
@@ -267,6 +268,7 @@ __global__ __launch_bounds__(R16_THREADS) void rows16_q4k(const Planes p, int64_
     int badrow = 0;
     auto last = [&](int b) { return b < c1 ? b : c1 - 1; };
 
+    const uint32_t k6464 = opaque(0x64006400u);  // in a register, so the nibble masks fuse into v_and_or_b32
     const v4f zero = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
     auto compute = [&](const uint8_t *cur) {
         R16W cw[TPW];
@@ -288,7 +290,7 @@ __global__ __launch_bounds__(R16_THREADS) void rows16_q4k(const Planes p, int64_
             const v8h al = reinterpret_cast<const v8h *>(cur + R16_PLANE)[64 * s + lane];
             v8h q[TPW];
 #pragma unroll
-            for (int tt = 0; tt < TPW; tt++) q[tt] = r16_codes(cw[tt], k[tt], s);
+            for (int tt = 0; tt < TPW; tt++) q[tt] = r16_codes(cw[tt], k[tt], s, k6464);
 #pragma unroll
             for (int tt = 0; tt < TPW; tt++) D[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, q[tt], D[tt], 0, 0, 0);
 #pragma unroll
