@@ -283,9 +283,13 @@ def profile_kernel(a):
         return 0
     tb = QuantBackend(0)
     if a.profile_kernel == "mfma":
-        for v in (0, 6, 8):
-            _ = mfma_rate(tb, v, 2)
-        print(json.dumps({"profiled": "mfma_probe", "valu_per_mfma": [0, 6, 8], "waves_per_simd": 2}))
+        # int8 TOPS (events) for VALU per MFMA 0..16 at one and two waves per SIMD: how much VALU work hides under
+        # the matrix cores, the ceiling of the act-quant prefill kernels
+        curve = {}
+        for w in (1, 2):
+            for v in (0, 2, 4, 6, 8, 12, 16):
+                curve["%d waves/SIMD, %d VALU/MFMA" % (w, v)] = round(mfma_rate(tb, v, w, iters=20000), 1)
+        print(json.dumps({"profiled": "mfma_probe", "int8_tops": curve, "peak_tops": INT8_PEAK_TOPS}))
         tb.close()
         return 0
     if a.profile_kernel == "sweep":

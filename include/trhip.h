@@ -211,9 +211,10 @@ int trhip_mfma_probe(trhip_ctx *ctx, int valu_per_mfma, int waves_per_simd, int6
  * (blocks in flight, waves, K parts, rows per lane); TRHIP_KNOB_EXACT_ROWS: exact four-lane GEMV rows
  * per workgroup a; TRHIP_KNOB_EXACT_LANES: exact GEMV lanes per row a; TRHIP_KNOB_ACTQ_TM: act-quant
  * MFMA row tile a; TRHIP_KNOB_ROWS16: fast q4_k kernel for 2..16 activation rows (a, b) = (16-row tiles per
- * wave 1 or 2; K slices 1..64, clamped to the block count). */
+ * wave 1 or 2; K slices 1..64, clamped to the block count); TRHIP_KNOB_KL_GRID: at least a workgroups for
+ * the K-across-lanes fast GEMV (its rows dealt over more, shorter row groups). */
 enum { TRHIP_KNOB_KL = 1, TRHIP_KNOB_FAST_Q4K = 2, TRHIP_KNOB_EXACT_ROWS = 3, TRHIP_KNOB_EXACT_LANES = 4,
-       TRHIP_KNOB_ACTQ_TM = 5, TRHIP_KNOB_ROWS16 = 6 };
+       TRHIP_KNOB_ACTQ_TM = 5, TRHIP_KNOB_ROWS16 = 6, TRHIP_KNOB_KL_GRID = 7 };
 int trhip_set_launch_shape(trhip_ctx *ctx, int knob, int a, int b, int c, int d);
 
 #ifdef __cplusplus

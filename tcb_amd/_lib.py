@@ -63,7 +63,7 @@ SIGNATURES = [
 OK, ERR_INVALID, ERR_OOM, ERR_HIP, ERR_LAUNCH, ERR_UNSUPPORTED, ERR_NO_DEVICE, ERR_BAD_SCALE = range(8)
 Q8, Q4, Q4K, Q6K = 1, 2, 3, 4
 MODE_EXACT, MODE_FAST = 0, 1
-KNOB_KL, KNOB_FAST_Q4K, KNOB_EXACT_ROWS, KNOB_EXACT_LANES, KNOB_ACTQ_TM, KNOB_ROWS16 = 1, 2, 3, 4, 5, 6
+KNOB_KL, KNOB_FAST_Q4K, KNOB_EXACT_ROWS, KNOB_EXACT_LANES, KNOB_ACTQ_TM, KNOB_ROWS16, KNOB_KL_GRID = 1, 2, 3, 4, 5, 6, 7
 
 
 def load(path=LIB_PATH):

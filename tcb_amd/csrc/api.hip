@@ -398,7 +398,7 @@ int trhip_set_launch_shape(trhip_ctx *ctx, int knob, int a, int b, int c, int d)
     switch (knob) {
     case TRHIP_KNOB_KL: {  // WAVES, KS, PD, RPW: the instantiated K-across-lanes shapes
         const int code = 1000 * a + 100 * b + 10 * c + d / 8;
-        static const int ok[] = {4141, 4142, 4122, 8141, 4242, 4241, 8241, 8441};
+        static const int ok[] = {4141, 4142, 4122, 8141, 4242, 4241, 8241, 8441, 4181, 8181, 2181, 4182, 16181, 4441, 8442};
         bool found = reset;
         for (int v : ok) found = found || (v == code && d % 8 == 0);
         if (!found) return fail(ctx, TRHIP_ERR_INVALID, "set_launch_shape: no such K-across-lanes shape");
@@ -428,6 +428,11 @@ int trhip_set_launch_shape(trhip_ctx *ctx, int knob, int a, int b, int c, int d)
         if (!(reset || ((a == 32 || a == 64) && !b && !c && !d)))
             return fail(ctx, TRHIP_ERR_INVALID, "set_launch_shape: act-quant row tile must be 32 or 64");
         ctx->force_actq_tm = a;
+        return TRHIP_OK;
+    case TRHIP_KNOB_KL_GRID:
+        if (!(reset || (a >= 1 && a <= 65536 && !b && !c && !d)))
+            return fail(ctx, TRHIP_ERR_INVALID, "set_launch_shape: K-across-lanes grid takes 1..65536 workgroups");
+        ctx->kl_min_wgs = a;
         return TRHIP_OK;
     case TRHIP_KNOB_ROWS16:
         if (!(reset || ((a == 1 || a == 2) && b >= 1 && b <= 64 && !c && !d)))

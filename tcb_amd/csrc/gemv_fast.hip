@@ -637,7 +637,8 @@ int run_kl(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const
     constexpr int RG = WAVES / KS;
     if (!kl_fits(DT, w->nb, KS)) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv_kl: K parts too long for the lanes of a wave");
     constexpr int OPW = SWI ? RPW / 2 : RPW;  // outputs per row group (SWI: two rows per output)
-    const int64_t wgs = (N + RG * OPW - 1) / (RG * OPW);  // every row group gets at most RPW rows
+    int64_t wgs = (N + RG * OPW - 1) / (RG * OPW);  // every row group gets at most RPW rows
+    if (ctx->kl_min_wgs > wgs) wgs = ctx->kl_min_wgs;  // more, shorter row groups (forced for tuning)
     if (N >= (int64_t)1 << 30 || wgs * RG >= (int64_t)1 << 31)
         return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv_kl: more than 2^30 rows");
     dim3 grid((unsigned)wgs), block(64 * WAVES);
@@ -696,6 +697,13 @@ int kl_forced(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, co
     case 4241: return run_kl<DT, 4, 2, 4, 8>(ctx, w, row0, N, x, c, acc);
     case 8241: return run_kl<DT, 8, 2, 4, 8>(ctx, w, row0, N, x, c, acc);
     case 8441: return run_kl<DT, 8, 4, 4, 8>(ctx, w, row0, N, x, c, acc);
+    case 4181: return run_kl<DT, 4, 1, 8, 8>(ctx, w, row0, N, x, c, acc);
+    case 8181: return run_kl<DT, 8, 1, 8, 8>(ctx, w, row0, N, x, c, acc);
+    case 2181: return run_kl<DT, 2, 1, 8, 8>(ctx, w, row0, N, x, c, acc);
+    case 4182: return run_kl<DT, 4, 1, 8, 16>(ctx, w, row0, N, x, c, acc);
+    case 16181: return run_kl<DT, 16, 1, 8, 8>(ctx, w, row0, N, x, c, acc);
+    case 4441: return run_kl<DT, 4, 4, 4, 8>(ctx, w, row0, N, x, c, acc);
+    case 8442: return run_kl<DT, 8, 4, 4, 16>(ctx, w, row0, N, x, c, acc);
     }
     return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv_kl: no such launch shape");
 }

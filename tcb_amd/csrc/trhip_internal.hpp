@@ -222,6 +222,7 @@ struct trhip_ctx {
     size_t up_slot_bytes = 0;
     // Launch-shape overrides set by trhip_set_launch_shape (tests and tuning only); 0 = the built-in choice.
     int force_kl = 0;           // K-across-lanes GEMV: 1000 WAVES + 100 KS + 10 PD + RPW / 8
+    int kl_min_wgs = 0;         // K-across-lanes GEMV: at least this many workgroups (0: built-in)
     int force_fast_q4k = 0;     // row-sliced fast q4_k GEMV: 1000 D + 100 WAVES + 10 KS + R
     int force_exact_rows = 0;   // exact four-lane GEMV rows per workgroup (16, 32, 64)
     int force_exact_lanes = 0;  // exact GEMV lanes per row (4, 8)
