@@ -248,22 +248,26 @@ def shape_table(tb):
         ob.free()
     emb.release()
     prefill = {}
-    for n, k in ((14336, 4096), (4096, 14336)):
-        w = tb.FromQuantized(Q4K, synth.random_blocks(Q4K, n, k, seed=7), n, k)
-        for M in (128, 512, 2048):
-            Xb = ctx.to_device(synth.activations(M, k, seed=8))
-            Cb = ctx.alloc(M * n * 4)
-            tb.GemmActQuant(M, n, k, Xb, w, Cb, accumulate=False)
+    cases = [(Q4K, 14336, 4096, M) for M in (128, 512, 2048)] + [(Q4K, 4096, 14336, M) for M in (128, 512, 2048)] + \
+            [(Q6K, 14336, 4096, 512), (Q4, 14336, 4096, 512)]
+    for dt, n, k, M in cases:
+        w = tb.FromQuantized(dt, synth.random_blocks(dt, n, k, seed=7), n, k)
+        Xb = ctx.to_device(synth.activations(M, k, seed=8))
+        Cb = ctx.alloc(M * n * 4)
+        res = {}
+        for md in ((MODE_FAST, MODE_EXACT) if dt == Q4K else (MODE_EXACT,)):
+            tb.GemmActQuant(M, n, k, Xb, w, Cb, accumulate=False, mode=md)
             ctx.sync()
-            g = capture(tb, lambda: tb.GemmActQuant(M, n, k, Xb, w, Cb, accumulate=False))
+            g = capture(tb, lambda: tb.GemmActQuant(M, n, k, Xb, w, Cb, accumulate=False, mode=md))
             time_graph(tb, g, 2)
             ms = time_graph(tb, g, 5) / 5
             L.trhip_graph_destroy(g)
             tops = 2.0 * M * n * k / (ms * 1e-3) / 1e12
-            prefill["q4_k %dx%d M=%d" % (n, k, M)] = {"us": round(ms * 1e3, 1), "int8_tops": round(tops, 1),
-                                                     "frac_of_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
-            Xb.free()
-            Cb.free()
+            res["fast" if md else "exact"] = {"us": round(ms * 1e3, 1), "int8_tops": round(tops, 1),
+                                              "frac_of_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+        prefill["%s %dx%d M=%d" % (names[dt], n, k, M)] = res
+        Xb.free()
+        Cb.free()
         w.release()
     return {"gemv_cold_ring": gemv, "rows": rows, "prefill": prefill, "open_q_and_embedding": other}
 
@@ -364,10 +368,11 @@ def profile_kernel(a):
         w = tb.FromQuantized(Q4K, raw, N, K)
         Xb = tb.ctx.to_device(synth.activations(M, K, seed=5))
         Cb = tb.ctx.alloc(M * N * 4)
+        mode = MODE_FAST if a.mode == "fast" else MODE_EXACT
         for _ in range(a.steps):
-            tb.GemmActQuant(M, N, K, Xb, w, Cb, accumulate=False)
+            tb.GemmActQuant(M, N, K, Xb, w, Cb, accumulate=False, mode=mode)
         tb.ctx.sync()
-        print(json.dumps({"profiled": "prefill_q4_k_M%d" % M, "launches": a.steps, "ops": 2 * M * N * K}))
+        print(json.dumps({"profiled": "prefill_q4_k_M%d_%s" % (M, a.mode), "launches": a.steps, "ops": 2 * M * N * K}))
     tb.close()
     return 0
 
@@ -520,19 +525,27 @@ def main():
         X = synth.activations(M, K, seed=5)
         Xb = ctx.to_device(X)
         Cb = ctx.alloc(M * N * 4)
-        tb.GemmActQuant(M, N, K, Xb, ring[0], Cb, accumulate=False)
-        ctx.sync()
-        gp = capture(tb, lambda: tb.GemmActQuant(M, N, K, Xb, ring[0], Cb, accumulate=False))
-        time_graph(tb, gp, 3)
-        reps = 10
-        ms = time_graph(tb, gp, reps) / reps
-        L.trhip_graph_destroy(gp)
+
+        def prefill_ms(md):
+            tb.GemmActQuant(M, N, K, Xb, ring[0], Cb, accumulate=False, mode=md)
+            ctx.sync()
+            gp = capture(tb, lambda: tb.GemmActQuant(M, N, K, Xb, ring[0], Cb, accumulate=False, mode=md))
+            time_graph(tb, gp, 3)
+            reps = 10
+            ms = time_graph(tb, gp, reps) / reps
+            L.trhip_graph_destroy(gp)
+            return ms
+
+        ms = prefill_ms(mode)
+        ms_other = prefill_ms(MODE_EXACT if mode == MODE_FAST else MODE_FAST)
         tops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
         ceiling = mfma_rate(tb, 0, 2)
         ceiling7 = mfma_rate(tb, 6, 2)
         prefill = {"workload": "act-quant GEMM q4_k %dx%d, M=%d (quantize + int block sums + fp32 epilogue)" % (N, K, M),
-                   "us": round(ms * 1e3, 2), "int8_tops": round(tops, 2),
+                   "mode": a.mode, "us": round(ms * 1e3, 2), "int8_tops": round(tops, 2),
                    "frac_of_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                   other_name + "_mode_us": round(ms_other * 1e3, 2),
+                   other_name + "_mode_frac_of_int8_peak": round(2.0 * M * N * K / (ms_other * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
                    "measured_int8_mfma_tops": round(ceiling, 1),
                    "measured_int8_mfma_tops_6valu": round(ceiling7, 1),
                    "frac_of_measured_int8": round(tops / ceiling, 4),

@@ -150,6 +150,14 @@ int trhip_gemm_q(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N,
 int trhip_gemm_q_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x,
                       float *c, int64_t M, int64_t K, int accumulate);
 
+/* trhip_gemm_q_actq with a mode, as trhip_gemm_q takes one (the reference's GemmActQuant has no mode; this is
+ * the same operator). TRHIP_MODE_EXACT is trhip_gemm_q_actq. TRHIP_MODE_FAST keeps the quantized activations and
+ * the exact int32 block sums (isum, msum) and fuses the per-block fp32 epilogue (two fma instead of two products,
+ * a difference and a sum) on the q4_k matrix-core kernels: deterministic and within 1e-4 of the exact result,
+ * |a - b| / (1 + |b|); other dtypes and small M run exact. */
+int trhip_gemm_q_actq_mode(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x,
+                           float *c, int64_t M, int64_t K, int accumulate, int mode);
+
 /* No counterpart in the reference: trhip_gemm_q_actq for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same arguments, kernels and bits as
  * trhip_gemm_q_actq, but the quantized activations live in a static device array of

@@ -49,6 +49,7 @@ SIGNATURES = [
     ("trhip_gemm_q", INT, [P, P, I64, I64, P, P, I64, I64, INT, INT]),
     ("trhip_gemm_q_actq", INT, [P, P, I64, I64, P, P, I64, I64, INT]),
     ("trhip_gemm_q_actq_noalloc", INT, [P, P, I64, I64, P, P, I64, I64, INT]),
+    ("trhip_gemm_q_actq_mode", INT, [P, P, I64, I64, P, P, I64, I64, INT, INT]),
     ("trhip_open_q", INT, [P, P, I64, I64, P]),
     ("trhip_read_probe", INT, [P, P, I64]),
     ("trhip_mfma_probe", INT, [P, INT, INT, I64]),

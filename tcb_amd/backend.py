@@ -223,8 +223,15 @@ class QuantBackend:
     def GemmSet(self, M, N, K, a, w, c, row0=0, mode=MODE_EXACT):
         _check(_lib.lib().trhip_gemm_q(self.ctx.h, w.h, row0, N, _ptr(a), _ptr(c), M, K, 0, mode), self.ctx.h)
 
-    def GemmActQuant(self, M, N, K, a, w, c, row0=0, accumulate=True):
-        _check(_lib.lib().trhip_gemm_q_actq(self.ctx.h, w.h, row0, N, _ptr(a), _ptr(c), M, K, 1 if accumulate else 0), self.ctx.h)
+    def GemmActQuant(self, M, N, K, a, w, c, row0=0, accumulate=True, mode=MODE_EXACT):
+        """ActQuantGemmer.GemmActQuant (tensor/matmul.go:59-61); mode=MODE_FAST fuses the fp32 epilogue over the same
+        exact integer block sums (trhip_gemm_q_actq_mode)."""
+        if mode == MODE_EXACT:
+            _check(_lib.lib().trhip_gemm_q_actq(self.ctx.h, w.h, row0, N, _ptr(a), _ptr(c), M, K, 1 if accumulate else 0),
+                   self.ctx.h)
+        else:
+            _check(_lib.lib().trhip_gemm_q_actq_mode(self.ctx.h, w.h, row0, N, _ptr(a), _ptr(c), M, K,
+                                                     1 if accumulate else 0, mode), self.ctx.h)
 
     def SwiGLU(self, gu, M, I, out):
         """out[m, i] = silu(gu[m, i]) * gu[m, I + i] (lib/layers.tr:223 on a merged [gate | up] output)."""

@@ -250,15 +250,18 @@ int launch_quantize_q8(trhip_ctx *ctx, const float *x, int64_t M, int64_t K, int
 constexpr int64_t kActqMfmaMinRows = 8;
 
 int launch_actq_mfma(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
-                     int64_t M, bool acc, const int8_t *q, const float *d, const uint16_t *sj, const uint8_t *bad);
+                     int64_t M, bool acc, const int8_t *q, const float *d, const uint16_t *sj, const uint8_t *bad,
+                     bool fast);
 
+// fast: the matrix-core kernel's fused epilogue (tolerance); the thread-per-output kernel is exact either way.
 int launch_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c, int64_t M,
-                bool acc, const int8_t *q, const float *d, const int16_t *bs, const uint8_t *bad, const uint16_t *sj) {
+                bool acc, const int8_t *q, const float *d, const int16_t *bs, const uint8_t *bad, const uint16_t *sj,
+                bool fast) {
     if (N == 0 || M == 0) return TRHIP_OK;
     switch (w->dtype) {
     case kQ4: return run_valu<kQ4>(ctx, w, row0, N, x, c, M, acc, q, d, bs, bad);
     case kQ4K:
-        if (M >= kActqMfmaMinRows && sj) return launch_actq_mfma(ctx, w, row0, N, x, c, M, acc, q, d, sj, bad);
+        if (M >= kActqMfmaMinRows && sj) return launch_actq_mfma(ctx, w, row0, N, x, c, M, acc, q, d, sj, bad, fast);
         return run_valu<kQ4K>(ctx, w, row0, N, x, c, M, acc, q, d, bs, bad);
     case kQ6K: return run_valu<kQ6K>(ctx, w, row0, N, x, c, M, acc, q, d, bs, bad);
     }

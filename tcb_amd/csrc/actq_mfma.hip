@@ -41,7 +41,8 @@ struct Tile {
 
 // msum = sum_j S_j m_j with S_j = 64 Sh_j + Sl_j: one f16 MFMA over k = [Sh_0..7 | Sl_0..7] x [64 m_0..7 | m_0..7].
 // Every product and partial sum is an integer below 2^24, so the fp32 result is msum exactly.
-template <bool ACC, int TM>
+// FAST: the same integer sums with the two products and the accumulation fused (within 1e-4 of the exact result).
+template <bool ACC, int TM, bool FAST>
 __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(TM == 64 ? 2 : 3, TM == 64 ? 2 : 4))) void actq_mfma_q4k(
     const Planes p, int64_t N, int64_t row0, int64_t M, int64_t K, const float *__restrict__ x,
     const int8_t *__restrict__ q, const float *__restrict__ d8, const uint16_t *__restrict__ sj,
@@ -172,8 +173,12 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(TM == 6
                 for (int r = 0; r < 4; r++) {
                     const int v = 4 * v4 + r;
                     const int isum = c0[t][v] + 8 * c1[t][v];
-                    const float tt = (dd * (float)isum) - (dm * cm[v]);
-                    accf[t][v] = accf[t][v] + tt * s8v[r];
+                    if (FAST) {
+                        accf[t][v] = fmaf(fmaf(-dm, cm[v], dd * (float)isum), s8v[r], accf[t][v]);
+                    } else {
+                        const float tt = (dd * (float)isum) - (dm * cm[v]);
+                        accf[t][v] = accf[t][v] + tt * s8v[r];
+                    }
                 }
             }
         }
@@ -208,17 +213,16 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(TM == 6
 
 template <int TM>
 int run_mfma(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c, int64_t M,
-             bool acc, const int8_t *q, const float *d, const uint16_t *sj, const uint8_t *bad) {
+             bool acc, const int8_t *q, const float *d, const uint16_t *sj, const uint8_t *bad, bool fast) {
     constexpr size_t lds = Tile<TM>::LDS;
     dim3 grid((unsigned)(((N + TN - 1) / TN) * ((M + TM - 1) / TM))), block(THREADS);
     static_assert(lds <= 64 * 1024, "below 64 KB of LDS no launch attribute is needed");
-    if (acc)
-        hipLaunchKernelGGL((actq_mfma_q4k<true, TM>), grid, block, lds, ctx->stream, w->planes(), N, row0, M, w->K, x, q, d,
-                           sj, bad, c);
-    else
-        hipLaunchKernelGGL((actq_mfma_q4k<false, TM>), grid, block, lds, ctx->stream, w->planes(), N, row0, M, w->K, x, q,
-                           d, sj, bad, c);
-    return launch_check(ctx, "actq_mfma_q4k");
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, block, lds, ctx->stream, w->planes(), N, row0, M, w->K, x, q, d, sj, bad, c);
+        return launch_check(ctx, "actq_mfma_q4k");
+    };
+    if (fast) return acc ? go(&actq_mfma_q4k<true, TM, true>) : go(&actq_mfma_q4k<false, TM, true>);
+    return acc ? go(&actq_mfma_q4k<true, TM, false>) : go(&actq_mfma_q4k<false, TM, false>);
 }
 
 // ---- Fast (tolerance) M > 1 path for q4_k: fp32 activations as three int8 digit planes ----
@@ -987,15 +991,16 @@ __global__ void fm_sum_swiglu_kernel(const float *__restrict__ partial, float *_
 }  // namespace
 
 int launch_actq_mfma(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
-                     int64_t M, bool acc, const int8_t *q, const float *d, const uint16_t *sj, const uint8_t *bad) {
+                     int64_t M, bool acc, const int8_t *q, const float *d, const uint16_t *sj, const uint8_t *bad,
+                     bool fast) {
     if (w->dtype != kQ4K) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "actq_mfma: q4_k only");
     // Row-tile height: 64 rows unless that leaves fewer than 160 workgroups (measured: 4096 x 14336 at M = 128
     // takes 74 us on 32-row tiles against 104 on 64; 14336 x 4096 at M = 128 or 512 is faster on 64).
     // trhip_set_launch_shape(TRHIP_KNOB_ACTQ_TM) overrides.
     const int64_t wgs64 = ((N + TN - 1) / TN) * ((M + 63) / 64);
     const int tm = ctx->force_actq_tm ? ctx->force_actq_tm : (wgs64 < 160 ? 32 : 64);
-    if (tm == 32) return run_mfma<32>(ctx, w, row0, N, x, c, M, acc, q, d, sj, bad);
-    return run_mfma<64>(ctx, w, row0, N, x, c, M, acc, q, d, sj, bad);
+    if (tm == 32) return run_mfma<32>(ctx, w, row0, N, x, c, M, acc, q, d, sj, bad, fast);
+    return run_mfma<64>(ctx, w, row0, N, x, c, M, acc, q, d, sj, bad, fast);
 }
 
 }  // namespace trhip

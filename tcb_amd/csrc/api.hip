@@ -879,7 +879,7 @@ int actq_check(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, c
 
 // Quantize x into the scratch `ws` (layout l) and run the integer block kernels.
 int actq_run(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c, int64_t M,
-             int64_t K, int accumulate, uint8_t *ws, const ActqLayout &l) {
+             int64_t K, int accumulate, uint8_t *ws, const ActqLayout &l, bool fast = false) {
     const int blk = block_elems(w->dtype);
     int8_t *q = reinterpret_cast<int8_t *>(ws + l.o_q);
     float *d = reinterpret_cast<float *>(ws + l.o_d);
@@ -896,11 +896,11 @@ int actq_run(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, con
     if (l.tiles) {
         int st = launch_quantize_tiles(ctx, xa, M, K, q, d, sj, bad);
         if (st != TRHIP_OK) return st;
-        return launch_prefill_q4k(ctx, w, row0, N, xa, c, M, accumulate != 0, q, d, sj, bad);
+        return launch_prefill_q4k(ctx, w, row0, N, xa, c, M, accumulate != 0, q, d, sj, bad, fast);
     }
     int st = launch_quantize_q8(ctx, xa, M, K, blk, q, d, bs, bad, sj);
     if (st != TRHIP_OK) return st;
-    return launch_actq(ctx, w, row0, N, xa, c, M, accumulate != 0, q, d, bs, bad, sj);
+    return launch_actq(ctx, w, row0, N, xa, c, M, accumulate != 0, q, d, bs, bad, sj, fast);
 }
 
 }  // namespace
@@ -931,9 +931,10 @@ int scratch_dev(trhip_ctx *ctx) {
 
 extern "C" {
 
-int trhip_gemm_q_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
-                      int64_t M, int64_t K, int accumulate) {
+int trhip_gemm_q_actq_mode(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
+                           int64_t M, int64_t K, int accumulate, int mode) {
     if (!ctx || !w) return TRHIP_ERR_INVALID;
+    if (mode != TRHIP_MODE_EXACT && mode != TRHIP_MODE_FAST) return fail(ctx, TRHIP_ERR_INVALID, "gemm_q_actq: unknown mode");
     int st = TRHIP_OK;
     const int r = actq_check(ctx, w, row0, N, x, c, M, K, "gemm_q_actq", &st);
     if (r) return st;
@@ -942,7 +943,12 @@ int trhip_gemm_q_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64
     const ActqLayout l = actq_layout(w->dtype, M, N, row0, K, x);
     uint8_t *ws = static_cast<uint8_t *>(workspace(ctx, l.total, &st));
     if (!ws) return st;
-    return actq_run(ctx, w, row0, N, x, c, M, K, accumulate, ws, l);
+    return actq_run(ctx, w, row0, N, x, c, M, K, accumulate, ws, l, mode == TRHIP_MODE_FAST);
+}
+
+int trhip_gemm_q_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
+                      int64_t M, int64_t K, int accumulate) {
+    return trhip_gemm_q_actq_mode(ctx, w, row0, N, x, c, M, K, accumulate, TRHIP_MODE_EXACT);
 }
 
 int trhip_gemm_q_actq_noalloc(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x,

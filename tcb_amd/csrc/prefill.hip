@@ -56,9 +56,20 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base, uin
 #define BUF_TO_LDS(SIZE, IMM, r, voffset, soffset, l) \
     __builtin_amdgcn_raw_ptr_buffer_load_lds((r), (lds_ptr)(l), SIZE, (voffset), (soffset), IMM, 0)
 
+// The per-block epilogue of one output: exact, in the reference's rounding order (seven VALU), or FAST, the same
+// integer sums with the two products and the accumulation fused (five VALU; within 1e-4 of the exact result).
+template <bool FAST>
+__device__ __forceinline__ float pf_epilogue(float acc, int p0, int p1, float cm, float dd, float dm, float d8) {
+    const int isum = p0 + 8 * p1;
+    if (FAST) return fmaf(fmaf(-dm, cm, dd * (float)isum), d8, acc);
+    const float tt = (dd * (float)isum) - (dm * cm);
+    return acc + tt * d8;
+}
+
 // One 32-row tile of a block: 16 int8 MFMAs into (c0, c1), and between them the epilogue of the pending tile held in
 // (p0, p1) with msum pcm, the pending block's d, dmin and the d8 of its rows (pd8, this lane's rows at + 8 (v / 4)
-// + (v % 4)): two outputs after each MFMA pair, in the reference's rounding order.
+// + (v % 4)): two outputs after each MFMA pair.
+template <bool FAST>
 __device__ __forceinline__ void pf_tile(v16i &c0, v16i &c1, const v16i &p0, const v16i &p1, const v16f &pcm, float pdd,
                                         float pdm, float *pacc, const float *pd8, const v4i *ar, const v4i (&b0)[8],
                                         const v4i (&b1)[8]) {
@@ -81,22 +92,21 @@ __device__ __forceinline__ void pf_tile(v16i &c0, v16i &c1, const v16i &p0, cons
 #pragma unroll
         for (int r = 0; r < 2; r++) {
             const int v = 2 * kc + r;
-            const int isum = p0[v] + 8 * p1[v];
-            const float tt = (pdd * (float)isum) - (pdm * pcm[v]);
-            pacc[v] = pacc[v] + tt * s8v[r];
+            pacc[v] = pf_epilogue<FAST>(pacc[v], p0[v], p1[v], pcm[v], pdd, pdm, s8v[r]);
         }
         // LDS reads first, then each MFMA followed by one output's epilogue
+        constexpr int EV = FAST ? 5 : 7;
         const int nreads = (kc + 1 < 8) + (kc + 2 < 8);
         if (nreads == 2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
         else if (nreads == 1) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, EV, 0);
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, EV, 0);
     }
 }
 
-template <bool ACC>
+template <bool ACC, bool FAST>
 __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_q4k(
     const Planes p, int64_t N, int64_t row0, int64_t M, int64_t K, const float *__restrict__ x,
     const int8_t *__restrict__ qt, const float *__restrict__ dt, const uint16_t *__restrict__ st,
@@ -226,25 +236,22 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
         const float *d8b = reinterpret_cast<const float *>(lds + T::DOFF + (b % 3) * T::D) + lrow;
         const float *d8p = reinterpret_cast<const float *>(lds + T::DOFF + ((b + 2) % 3) * T::D) + lrow;
         // tiles 0..3 in sets x, y, x, y; each one's epilogue runs inside the next tile
-        pf_tile(x0, x1, y0, y1, pcm, pdd, pdm, accf[MT - 1], d8p + 32 * (MT - 1), ar, b0, b1);
+        pf_tile<FAST>(x0, x1, y0, y1, pcm, pdd, pdm, accf[MT - 1], d8p + 32 * (MT - 1), ar, b0, b1);
         pcm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[0], bmv, (v16f){0.0f}, 0, 0, 0);
         pdd = dd;
         pdm = dm;
-        pf_tile(y0, y1, x0, x1, pcm, pdd, pdm, accf[0], d8b, ar + 512, b0, b1);
+        pf_tile<FAST>(y0, y1, x0, x1, pcm, pdd, pdm, accf[0], d8b, ar + 512, b0, b1);
         pcm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[64], bmv, (v16f){0.0f}, 0, 0, 0);
-        pf_tile(x0, x1, y0, y1, pcm, pdd, pdm, accf[1], d8b + 32, ar + 1024, b0, b1);
+        pf_tile<FAST>(x0, x1, y0, y1, pcm, pdd, pdm, accf[1], d8b + 32, ar + 1024, b0, b1);
         pcm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[128], bmv, (v16f){0.0f}, 0, 0, 0);
-        pf_tile(y0, y1, x0, x1, pcm, pdd, pdm, accf[2], d8b + 64, ar + 1536, b0, b1);
+        pf_tile<FAST>(y0, y1, x0, x1, pcm, pdd, pdm, accf[2], d8b + 64, ar + 1536, b0, b1);
         pcm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[192], bmv, (v16f){0.0f}, 0, 0, 0);
     }
     {  // the last block's last tile (set y)
         const float *d8l = reinterpret_cast<const float *>(lds + T::DOFF + ((nb + 2) % 3) * T::D) + lrow + 32 * (MT - 1);
 #pragma unroll
-        for (int v = 0; v < 16; v++) {
-            const int isum = y0[v] + 8 * y1[v];
-            const float tt = (pdd * (float)isum) - (pdm * pcm[v]);
-            accf[MT - 1][v] = accf[MT - 1][v] + tt * d8l[8 * (v >> 2) + (v & 3)];
-        }
+        for (int v = 0; v < 16; v++)
+            accf[MT - 1][v] = pf_epilogue<FAST>(accf[MT - 1][v], y0[v], y1[v], pcm[v], pdd, pdm, d8l[8 * (v >> 2) + (v & 3)]);
     }
 
     const int64_t gn = n0 + nloc;
@@ -291,23 +298,22 @@ bool prefill_tiles_apply(int dtype, int64_t M, int64_t N, int64_t row0, int64_t 
 }
 
 int launch_prefill_q4k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
-                       int64_t M, bool acc, const int8_t *qt, const float *dt, const uint16_t *st, const uint8_t *bad) {
+                       int64_t M, bool acc, const int8_t *qt, const float *dt, const uint16_t *st, const uint8_t *bad,
+                       bool fast) {
     using T = Pf;
     static_assert(T::TM == kPrefillRowPad, "the tiled layout pads rows to one workgroup row tile");
     const int64_t wgs = ((M + T::TM - 1) / T::TM) * ((N + PF_TN - 1) / PF_TN);
     if (wgs >= ((int64_t)1 << 31)) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "prefill: grid too large");
     if (!prefill_fits32(M, N, row0, w->K)) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "prefill: buffers above 4 GB");
-    const void *fn = acc ? reinterpret_cast<const void *>(&prefill_q4k<true>)
-                         : reinterpret_cast<const void *>(&prefill_q4k<false>);
-    int st0 = allow_dyn_lds(ctx, fn, T::LDS, "prefill: LDS size");
-    if (st0 != TRHIP_OK) return st0;
-    if (acc)
-        hipLaunchKernelGGL((prefill_q4k<true>), dim3((unsigned)wgs), dim3(PF_THREADS), T::LDS, ctx->stream,
-                           w->planes(), N, row0, M, w->K, x, qt, dt, st, bad, c);
-    else
-        hipLaunchKernelGGL((prefill_q4k<false>), dim3((unsigned)wgs), dim3(PF_THREADS), T::LDS, ctx->stream,
-                           w->planes(), N, row0, M, w->K, x, qt, dt, st, bad, c);
-    return launch_check(ctx, "prefill_q4k");
+    auto go = [&](auto kern) {
+        int st0 = allow_dyn_lds(ctx, reinterpret_cast<const void *>(kern), T::LDS, "prefill: LDS size");
+        if (st0 != TRHIP_OK) return st0;
+        hipLaunchKernelGGL(kern, dim3((unsigned)wgs), dim3(PF_THREADS), T::LDS, ctx->stream, w->planes(), N, row0, M,
+                           w->K, x, qt, dt, st, bad, c);
+        return launch_check(ctx, "prefill_q4k");
+    };
+    if (fast) return acc ? go(&prefill_q4k<true, true>) : go(&prefill_q4k<false, true>);
+    return acc ? go(&prefill_q4k<true, false>) : go(&prefill_q4k<false, false>);
 }
 
 }  // namespace trhip

@@ -288,8 +288,10 @@ int launch_read_probe(trhip_ctx *ctx, const void *p, int64_t bytes);
 bool prefill_tiles_apply(int dtype, int64_t M, int64_t N, int64_t row0, int64_t K);
 int launch_quantize_tiles(trhip_ctx *ctx, const float *x, int64_t M, int64_t K, int8_t *qt, float *dt, uint16_t *st,
                           uint8_t *bad);
+// fast: the same exact integer block sums with the fp32 epilogue fused (tolerance mode); else bit-exact.
 int launch_prefill_q4k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
-                       int64_t M, bool acc, const int8_t *qt, const float *dt, const uint16_t *st, const uint8_t *bad);
+                       int64_t M, bool acc, const int8_t *qt, const float *dt, const uint16_t *st, const uint8_t *bad,
+                       bool fast);
 int launch_mfma_probe(trhip_ctx *ctx, int valu_per_mfma, int waves_per_simd, int64_t iters);
 // Fast-mode q4_k product for 1 <= M <= 16 activation rows in one launch (rows16.hip); swi as in
 // launch_gemm_rows_fast. Returns -1 (nothing launched) where it does not apply.
@@ -297,5 +299,5 @@ int launch_rows16_q4k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64
                       int64_t M, bool acc, float *swi = nullptr);
 int launch_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                 int64_t M, bool acc, const int8_t *q, const float *d, const int16_t *bs, const uint8_t *bad,
-                const uint16_t *sj);
+                const uint16_t *sj, bool fast);
 }  // namespace trhip

@@ -24,7 +24,8 @@ def declared():
 
 def test_header_declares_the_boundary():
     names = declared()
-    for must in ("trhip_init", "trhip_wstore_create", "trhip_gemm_q", "trhip_gemm_q_actq", "trhip_open_q",
+    for must in ("trhip_init", "trhip_wstore_create", "trhip_gemm_q", "trhip_gemm_q_actq", "trhip_gemm_q_actq_mode",
+                 "trhip_open_q",
                  "trhip_embedding_q", "trhip_check_quant_scales", "trhip_strerror", "trhip_last_error"):
         assert must in names
 
@@ -78,6 +79,7 @@ def test_null_context_is_refused():
     lib = _lib.lib()
     assert lib.trhip_gemm_q(None, None, 0, 1, None, None, 1, 32, 1, 0) != 0
     assert lib.trhip_gemm_q_actq(None, None, 0, 1, None, None, 1, 256, 1) != 0
+    assert lib.trhip_gemm_q_actq_mode(None, None, 0, 1, None, None, 1, 256, 1, 1) != 0
     assert lib.trhip_sync(None) != 0
 
 

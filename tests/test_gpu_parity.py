@@ -458,6 +458,107 @@ def test_actq_prefill_sizes_bits(backend, N, K, M):
     w.release()
 
 
+def _q4k_weights_f64(raw, N, K):
+    """q4_k weights d (sc q) - dmin m in float64 without the fp32 roundings of the dequant: sc q and m are recovered
+    exactly as the dequant of the same blocks with (d, dmin) set to (1, 0) and (0, 1), and d, dmin read from the
+    blocks' fp16 fields."""
+    blk = np.array(raw, np.uint8).reshape(-1, 144)
+    one, zero = np.array([0x00, 0x3C], np.uint8), np.array([0, 0], np.uint8)  # fp16 1.0 and +0
+    a, b = blk.copy(), blk.copy()
+    a[:, 0:2], a[:, 2:4] = one, zero
+    b[:, 0:2], b[:, 2:4] = zero, one
+    scq = O.dequant(Q4K, a.reshape(-1)).astype(np.float64).reshape(-1, 256)
+    negm = O.dequant(Q4K, b.reshape(-1)).astype(np.float64).reshape(-1, 256)
+    d = blk[:, 0:2].copy().view(np.float16).astype(np.float64)
+    dmin = blk[:, 2:4].copy().view(np.float16).astype(np.float64)
+    return (d * scq + dmin * negm).reshape(N, K)
+
+
+def _run_actq_modes(backend, raw, X, M, N, K, row0, c0, acc):
+    """Fast twice and exact once on the same inputs; returns the three outputs as [M, N]."""
+    w = backend.FromQuantized(Q4K, raw, row0 + N, K)
+    xb = backend.ctx.to_device(X)
+    outs = []
+    for md in (MODE_FAST, MODE_FAST, MODE_EXACT):
+        cb = backend.ctx.to_device(c0)
+        backend.GemmActQuant(M, N, K, xb, w, cb, row0=row0, accumulate=acc, mode=md)
+        outs.append(cb.download(np.float32, M * N).reshape(M, N))
+        cb.free()
+    xb.free()
+    w.release()
+    return outs
+
+
+@pytest.mark.parametrize("M,N,K,row0,acc", [(8, 64, 256, 0, True), (130, 70, 512, 0, False), (300, 16421, 512, 5, True),
+                                            (384, 12800, 1024, 0, False), (128, 14336, 4096, 0, False),
+                                            (512, 14336, 4096, 0, False), (512, 4096, 14336, 0, True),
+                                            (2048, 4096, 14336, 0, False)])
+def test_actq_fast_within_tolerance(backend, M, N, K, row0, acc):
+    """Fast act-quant (trhip_gemm_q_actq_mode) on encoded model weights: the same quantized activations and exact
+    integer block sums with the fp32 epilogue fused, on both matrix-core kernels (64-row tiles below, 128 rows
+    per wave from 192 128x256 tiles up): within the K-quant bound 1e-4 of quantGemmAct by |a-b|/(1+|b|), the same
+    bits on every call, NaN rows as the exact path computes them (fp32 fallback), and different bits from the exact
+    mode somewhere (the fused kernel ran). The x1000 row is compared at its input's scale (both results divided by
+    1000), as the fast GEMV tests compare theirs: its outputs are 1000 times larger, so an output that cancels to
+    a small value carries rounding at the 1000-fold scale in either order."""
+    rng = _rng(M + N + K + 7)
+    raw = _ffn_q4k(N, K) if (N, K) in ((14336, 4096), (4096, 14336)) and row0 == 0 else \
+        synth.quant_weights(Q4K, row0 + N, K, seed=M + K, outliers=0.01)
+    X = _x(rng, M * K).reshape(M, K)
+    X[1] *= 1000
+    X[2, :256] = 0
+    X[M - 2, 11] = np.nan
+    c0 = _x(rng, M * N) if acc else np.zeros(M * N, np.float32)
+    fast, fast2, exact = _run_actq_modes(backend, raw, X, M, N, K, row0, c0, acc)
+    same_bits(fast, fast2)
+    rows = np.ascontiguousarray(raw.reshape(row0 + N, -1)[row0:])
+    want = O.quant_gemm_act(Q4K, M, N, K, X, rows, c0).reshape(M, N)
+    same_bits(exact, want)
+    same_bits(fast[M - 2], want[M - 2])
+    fin = np.ones(M, bool)
+    fin[M - 2] = False
+    fin[1] = False
+    assert rel_err(fast[fin], want[fin]) <= 1e-4
+    assert rel_err(fast[1] / np.float32(1000), want[1] / np.float32(1000)) <= 1e-4
+    assert not np.array_equal(fast[fin].view(np.uint32), want[fin].view(np.uint32))
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 300, 1024), (384, 12800, 1024), (512, 2048, 4096)])
+def test_actq_fast_random_scale_blocks(backend, M, N, K):
+    """Fast act-quant on TR's random-scale blocks (cpu_quant_test.go:71-86), whose rows cancel: d isum and
+    dmin msum nearly cancel inside each block, so any fp32 rounding order of the epilogue lands ulps of the large
+    terms apart. Held to the standard of the fast GEMV on these blocks: against the float64 value of the same
+    quantized product (q8 codes times their scales, times the dequantized weights: the value both epilogues round),
+    the fast result is no further than 1e-4 or twice the exact path's own distance, whichever is larger."""
+    rng = _rng(M * 3 + K)
+    raw = _weights(Q4K, N, K, N + K + M)
+    X = _x(rng, M * K).reshape(M, K)
+    c0 = np.zeros(M * N, np.float32)
+    fast, fast2, exact = _run_actq_modes(backend, raw, X, M, N, K, 0, c0, False)
+    same_bits(fast, fast2)
+    same_bits(exact, O.quant_gemm_act(Q4K, M, N, K, X, raw))
+    q, d8, _ = O.quantize_q8(X, 256)
+    xq = (q.astype(np.float64).reshape(M, K // 256, 256) * d8.astype(np.float64).reshape(M, K // 256, 1)).reshape(M, K)
+    truth = xq @ _q4k_weights_f64(raw, N, K).T
+    fast_err, exact_err = rel_err(fast, truth), rel_err(exact, truth)
+    assert fast_err <= max(1e-4, 2.0 * exact_err), (M, N, K, fast_err, exact_err)
+
+
+@pytest.mark.parametrize("dt", [Q4, Q6K])
+def test_actq_fast_other_dtypes_exact(backend, dt):
+    """q4_0 and q6_k act-quant have no fused epilogue: fast mode gives the exact bits."""
+    M, N, K = 16, 300, 2048
+    raw = _weights(dt, N, K, 5)
+    X = _x(_rng(9), M * K).reshape(M, K)
+    w = backend.FromQuantized(dt, raw, N, K)
+    xb, cb = backend.ctx.to_device(X), backend.ctx.alloc(M * N * 4)
+    backend.GemmActQuant(M, N, K, xb, w, cb, accumulate=False, mode=MODE_FAST)
+    same_bits(cb.download(np.float32, M * N), O.quant_gemm_act(dt, M, N, K, X, raw))
+    for b in (xb, cb):
+        b.free()
+    w.release()
+
+
 @pytest.mark.parametrize("dt", DTS)
 @pytest.mark.parametrize("M", [97, 128])
 def test_gemm_rows_above_panel_bits(backend, dt, M):
