@@ -263,7 +263,9 @@ int launch_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, 
     case kQ4K:
         if (M >= kActqMfmaMinRows && sj) return launch_actq_mfma(ctx, w, row0, N, x, c, M, acc, q, d, sj, bad, fast);
         return run_valu<kQ4K>(ctx, w, row0, N, x, c, M, acc, q, d, bs, bad);
-    case kQ6K: return run_valu<kQ6K>(ctx, w, row0, N, x, c, M, acc, q, d, bs, bad);
+    case kQ6K:
+        if (actq6_mfma_applies(M, N, row0, w->K)) return launch_actq6_mfma(ctx, w, row0, N, x, c, M, acc, q, d, bad);
+        return run_valu<kQ6K>(ctx, w, row0, N, x, c, M, acc, q, d, bs, bad);
     }
     return fail(ctx, TRHIP_ERR_UNSUPPORTED, "actq: dtype must be q4, q4_k or q6_k");
 }

@@ -395,6 +395,51 @@ def test_actq_tiles_bits(backend, M, N, K, row0, acc):
     w.release()
 
 
+@pytest.mark.parametrize("M,N,K,row0,acc", [(8, 16, 256, 0, True), (130, 70, 512, 0, False), (257, 129, 1024, 5, True),
+                                            (16, 200, 4096, 0, True), (128, 128, 256, 64, False), (300, 1, 512, 0, True),
+                                            (64, 1000, 2048, 3, False)])
+def test_actq_q6k_tiles_bits(backend, M, N, K, row0, acc):
+    """q6_k act-quant on the int8 matrix cores (128 x 128 tiles, sub-block sums through zero-masked 16x16x64
+    products): row counts that fill, straddle and overhang the tiles, ragged N, a row slice of the store, both
+    accumulate modes, x1000 / zero / +-1 rows and one NaN row inside a tile, on TR's random-scale blocks (signed
+    sub-block scales of every magnitude): bit-identical to quantGemmAct."""
+    rng = _rng(M * 5 + N * 3 + K + row0)
+    raw = _weights(Q6K, row0 + N, K, M + N + K + 1)
+    X = _x(rng, M * K).reshape(M, K)
+    for m in range(M):
+        if m % 7 == 1:
+            X[m] *= 1000
+        elif m % 7 == 2:
+            X[m, :256] = 0
+        elif m % 7 == 3:
+            X[m] = 1 - 2 * (np.arange(K) % 2)
+    if M > 20:
+        X[M // 2, 3] = np.nan
+    w = backend.FromQuantized(Q6K, raw, row0 + N, K)
+    c0 = _x(rng, M * N) if acc else np.zeros(M * N, np.float32)
+    xb, cb = backend.ctx.to_device(X), backend.ctx.to_device(c0)
+    backend.GemmActQuant(M, N, K, xb, w, cb, row0=row0, accumulate=acc)
+    rows = np.ascontiguousarray(raw.reshape(row0 + N, -1)[row0:])
+    same_bits(cb.download(np.float32, M * N), O.quant_gemm_act(Q6K, M, N, K, X, rows, c0))
+    for b in (xb, cb):
+        b.free()
+    w.release()
+
+
+@pytest.mark.parametrize("N,K,M", [(14336, 4096, 512), (4096, 14336, 128)])
+def test_actq_q6k_prefill_bits(backend, N, K, M):
+    """q6_k act-quant at prefill sizes on encoded model weights, every output compared: bit-identical."""
+    raw = synth.quant_weights(Q6K, N, K, seed=43, outliers=0.01)
+    X = synth.activations(M, K, seed=44 + M)
+    w = backend.FromQuantized(Q6K, raw, N, K)
+    xb, cb = backend.ctx.to_device(X), backend.ctx.alloc(M * N * 4)
+    backend.GemmActQuant(M, N, K, xb, w, cb, accumulate=False)
+    same_bits(cb.download(np.float32, M * N), O.quant_gemm_act(Q6K, M, N, K, X, raw))
+    for b in (xb, cb):
+        b.free()
+    w.release()
+
+
 @pytest.mark.parametrize("M,N,K,row0,acc,x_off", [(300, 16421, 512, 5, True, 0), (257, 49153, 256, 0, False, 4),
                                                   (384, 12800, 1024, 0, True, 0)])
 def test_prefill_tiles_bits(backend, M, N, K, row0, acc, x_off):
