@@ -259,7 +259,9 @@ int launch_actq(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, 
                 bool fast) {
     if (N == 0 || M == 0) return TRHIP_OK;
     switch (w->dtype) {
-    case kQ4: return run_valu<kQ4>(ctx, w, row0, N, x, c, M, acc, q, d, bs, bad);
+    case kQ4:
+        if (actq4_mfma_applies(M, N, row0, w->K)) return launch_actq4_mfma(ctx, w, row0, N, x, c, M, acc, q, d, bad);
+        return run_valu<kQ4>(ctx, w, row0, N, x, c, M, acc, q, d, bs, bad);
     case kQ4K:
         if (M >= kActqMfmaMinRows && sj) return launch_actq_mfma(ctx, w, row0, N, x, c, M, acc, q, d, sj, bad, fast);
         return run_valu<kQ4K>(ctx, w, row0, N, x, c, M, acc, q, d, bs, bad);

@@ -297,7 +297,10 @@ int launch_mfma_probe(trhip_ctx *ctx, int valu_per_mfma, int waves_per_simd, int
 // launch_gemm_rows_fast. Returns -1 (nothing launched) where it does not apply.
 int launch_rows16_q4k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                       int64_t M, bool acc, float *swi = nullptr);
-// q6_k act-quant on int8 matrix cores (actq6.hip): whether it takes the shape, and the kernel.
+// q4_0 and q6_k act-quant on int8 matrix cores (actq4.hip, actq6.hip): whether each takes the shape, and the kernel.
+bool actq4_mfma_applies(int64_t M, int64_t N, int64_t row0, int64_t K);
+int launch_actq4_mfma(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
+                      int64_t M, bool acc, const int8_t *q, const float *d, const uint8_t *bad);
 bool actq6_mfma_applies(int64_t M, int64_t N, int64_t row0, int64_t K);
 int launch_actq6_mfma(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                       int64_t M, bool acc, const int8_t *q, const float *d, const uint8_t *bad);

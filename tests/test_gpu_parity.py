@@ -426,15 +426,47 @@ def test_actq_q6k_tiles_bits(backend, M, N, K, row0, acc):
     w.release()
 
 
+@pytest.mark.parametrize("M,N,K,row0,acc", [(8, 16, 256, 0, True), (130, 70, 512, 0, False), (257, 129, 1024, 5, True),
+                                            (16, 200, 4096, 0, True), (64, 128, 256, 64, False), (300, 1, 512, 0, True),
+                                            (65, 1000, 2560, 3, False)])
+def test_actq_q4_0_tiles_bits(backend, M, N, K, row0, acc):
+    """q4_0 act-quant on the int8 matrix cores (one 32-element block per 32x32x32 product, 64 x 128 tiles, eight
+    blocks per LDS stage): row counts that fill, straddle and overhang the tiles, ragged N, a row slice of the store,
+    both accumulate modes, x1000 / zero / +-1 rows and one NaN row inside a tile, on TR's random-scale blocks:
+    bit-identical to quantGemmAct."""
+    rng = _rng(M * 7 + N * 5 + K + row0)
+    raw = _weights(Q4, row0 + N, K, M + N + K + 2)
+    X = _x(rng, M * K).reshape(M, K)
+    for m in range(M):
+        if m % 7 == 1:
+            X[m] *= 1000
+        elif m % 7 == 2:
+            X[m, :256] = 0
+        elif m % 7 == 3:
+            X[m] = 1 - 2 * (np.arange(K) % 2)
+    if M > 20:
+        X[M // 2, 3] = np.nan
+    w = backend.FromQuantized(Q4, raw, row0 + N, K)
+    c0 = _x(rng, M * N) if acc else np.zeros(M * N, np.float32)
+    xb, cb = backend.ctx.to_device(X), backend.ctx.to_device(c0)
+    backend.GemmActQuant(M, N, K, xb, w, cb, row0=row0, accumulate=acc)
+    rows = np.ascontiguousarray(raw.reshape(row0 + N, -1)[row0:])
+    same_bits(cb.download(np.float32, M * N), O.quant_gemm_act(Q4, M, N, K, X, rows, c0))
+    for b in (xb, cb):
+        b.free()
+    w.release()
+
+
+@pytest.mark.parametrize("dt", [Q4, Q6K])
 @pytest.mark.parametrize("N,K,M", [(14336, 4096, 512), (4096, 14336, 128)])
-def test_actq_q6k_prefill_bits(backend, N, K, M):
-    """q6_k act-quant at prefill sizes on encoded model weights, every output compared: bit-identical."""
-    raw = synth.quant_weights(Q6K, N, K, seed=43, outliers=0.01)
+def test_actq_prefill_other_dtypes_bits(backend, dt, N, K, M):
+    """q4_0 and q6_k act-quant at prefill sizes on encoded model weights, every output compared: bit-identical."""
+    raw = synth.quant_weights(dt, N, K, seed=43, outliers=0.01 if dt == Q6K else 0.0)
     X = synth.activations(M, K, seed=44 + M)
-    w = backend.FromQuantized(Q6K, raw, N, K)
+    w = backend.FromQuantized(dt, raw, N, K)
     xb, cb = backend.ctx.to_device(X), backend.ctx.alloc(M * N * 4)
     backend.GemmActQuant(M, N, K, xb, w, cb, accumulate=False)
-    same_bits(cb.download(np.float32, M * N), O.quant_gemm_act(Q6K, M, N, K, X, raw))
+    same_bits(cb.download(np.float32, M * N), O.quant_gemm_act(dt, M, N, K, X, raw))
     for b in (xb, cb):
         b.free()
     w.release()
