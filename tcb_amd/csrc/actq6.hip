@@ -29,21 +29,21 @@ namespace {
 
 constexpr int Q6_W = 8;                   // waves per workgroup
 constexpr int Q6_TN = 16 * Q6_W;          // weight rows per workgroup
-constexpr int Q6_MT = 8;                  // 16-row activation tiles per wave
-constexpr int Q6_TM = 16 * Q6_MT;         // activation rows per workgroup
 constexpr int Q6_THREADS = 64 * Q6_W;
+template <int MT>                         // MT 16-row activation tiles per wave
 struct Q6L {
-    static constexpr int ACT = Q6_TM * 256;   // activation codes of one block
+    static constexpr int TM = 16 * MT;        // activation rows per workgroup
+    static constexpr int ACT = TM * 256;      // activation codes of one block
     static constexpr int QL = Q6_TN * 128;    // ql bytes of the workgroup's weight rows
     static constexpr int QH = Q6_TN * 64;
     static constexpr int SC = Q6_TN * 16;
     static constexpr int DW = Q6_TN * 4;      // d of the weight rows, fp32
-    static constexpr int D8 = Q6_TM * 4;      // d8 of the activation rows
+    static constexpr int D8 = TM * 4;         // d8 of the activation rows
     static constexpr int O_QL = ACT, O_QH = O_QL + QL, O_SC = O_QH + QH, O_DW = O_SC + SC, O_D8 = O_DW + DW;
     static constexpr int STAGE = O_D8 + D8;
-    static constexpr size_t LDS = 2 * STAGE + (Q6_TM + 1) * sizeof(int);
+    static constexpr size_t LDS = 2 * STAGE + (TM + 1) * sizeof(int);
 };
-static_assert(Q6L::LDS <= 160 * 1024, "one workgroup per CU");
+static_assert(Q6L<8>::LDS <= 160 * 1024, "one workgroup per CU");
 
 typedef __attribute__((address_space(3))) void *q6_lds_ptr;
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t q6_rsrc(const void *base, uint32_t bytes) {
@@ -70,12 +70,13 @@ __device__ __forceinline__ uint32_t q6_codes(uint32_t L, uint32_t H) {
     return ((lo | hi) + 0x60606060u) ^ 0x80808080u;
 }
 
-template <bool ACC>
+template <bool ACC, int MT>
 __global__ __launch_bounds__(Q6_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void actq6_mfma(
     const Planes p, int64_t N, int64_t row0, int64_t M, int64_t K, const float *__restrict__ x,
     const int8_t *__restrict__ q, const float *__restrict__ d8g, const uint8_t *__restrict__ bad_blk,
     float *__restrict__ c) {
-    using L = Q6L;
+    using L = Q6L<MT>;
+    constexpr int Q6_TM = L::TM, Q6_MT = MT;
     extern __shared__ __align__(16) uint8_t lds[];
     int *rowstate = reinterpret_cast<int *>(lds + 2 * L::STAGE);  // [TM] 0 ok, 1 NaN/Inf row, 2 outside M
     int *anybad = rowstate + Q6_TM;
@@ -95,14 +96,15 @@ __global__ __launch_bounds__(Q6_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
     const __amdgpu_buffer_rsrc_t rsc = q6_rsrc(p.sc, (uint32_t)((row0 + N) * nb * 16));
     const int64_t wr0 = row0 + n0;  // the workgroup's first store row
 
-    // DMA offsets. Activation instruction j (32 per block, four per wave): rows 4 j .. 4 j + 3, lane L -> row
+    // DMA offsets. Activation instruction j (TM / 4 per block, TM / 32 per wave): rows 4 j .. 4 j + 3, lane L -> row
     // 4 j + L / 16, column (L % 16) ^ (row & 7). Weight ql instruction j (16 per block, two per wave): rows
     // 8 j .. +7, lane L -> row 8 j + L / 8, piece L % 8. qh (8, one per wave): rows 16 j + L / 4, piece L % 4. sc
     // (2, waves 0 and 1): row 64 j + L.
-    uint32_t va[4];
+    constexpr int AI = Q6_TM / 32;  // activation instructions per wave
+    uint32_t va[AI];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int j = 4 * w + i, row = 4 * j + (lane >> 4), col = (lane & 15) ^ (row & 7);
+    for (int i = 0; i < AI; i++) {
+        const int j = AI * w + i, row = 4 * j + (lane >> 4), col = (lane & 15) ^ (row & 7);
         va[i] = (uint32_t)((m0 + row) * K + 16 * col);
     }
     uint32_t vql[2];
@@ -120,7 +122,7 @@ __global__ __launch_bounds__(Q6_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
     auto stage = [&](int b, int buf) {
         uint8_t *sb = lds + buf * L::STAGE;
 #pragma unroll
-        for (int i = 0; i < 4; i++) q6_dma16(rq, va[i], (uint32_t)(256 * b), sb + 1024 * (4 * w + i));
+        for (int i = 0; i < AI; i++) q6_dma16(rq, va[i], (uint32_t)(256 * b), sb + 1024 * (AI * w + i));
 #pragma unroll
         for (int i = 0; i < 2; i++) q6_dma16(rql, vql[i], (uint32_t)(128 * b), sb + L::O_QL + 1024 * (2 * w + i));
         q6_dma16(rqh, vqh, (uint32_t)(64 * b), sb + L::O_QH + 1024 * w);
@@ -155,15 +157,15 @@ __global__ __launch_bounds__(Q6_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
 
     fetch_scales(0);
     stage(0, 0);
+    put_scales(0);
     for (int b = 0; b < nb; b++) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();  // block b is in stage b & 1; nobody reads the other stage any more
-        put_scales(b & 1);
+        // block b (DMA and scales) is in stage b & 1 once every load has landed; after the barrier nobody reads
+        // the other stage (block b - 1) any more
+        __syncthreads();
         if (b + 1 < nb) {
             fetch_scales(b + 1);
             stage(b + 1, (b + 1) & 1);
         }
-        __syncthreads();  // the scales of block b are in LDS
         const uint8_t *sb = lds + (b & 1) * L::STAGE;
         int X[4][Q6_MT];
 #pragma unroll
@@ -223,6 +225,9 @@ __global__ __launch_bounds__(Q6_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
                 acc[g4][t] = acc[g4][t] + tt * d8s[16 * t + ai];
             }
         }
+        // the next block's scales into the other stage (last read before this block's barrier); the next barrier
+        // publishes them
+        if (b + 1 < nb) put_scales((b + 1) & 1);
     }
 
 #pragma unroll
@@ -262,16 +267,21 @@ int launch_actq6_mfma(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64
                       int64_t M, bool acc, const int8_t *q, const float *d, const uint8_t *bad) {
     if (w->dtype != kQ6K) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "actq6_mfma: q6_k only");
     if (!actq6_mfma_applies(M, N, row0, w->K)) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "actq6_mfma: shape");
-    const int64_t wgs = ((M + Q6_TM - 1) / Q6_TM) * ((N + Q6_TN - 1) / Q6_TN);
-    if (wgs >= ((int64_t)1 << 31)) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "actq6_mfma: grid too large");
-    auto go = [&](auto kern) {
-        int st = allow_dyn_lds(ctx, reinterpret_cast<const void *>(kern), Q6L::LDS, "actq6_mfma: LDS size");
+    // 128 activation rows per workgroup, or 64 where 128 would leave CUs without a workgroup
+    const int cus = ctx->sm_count > 0 ? ctx->sm_count : 256;
+    const int64_t nt = (N + Q6_TN - 1) / Q6_TN;
+    const bool small = ((M + 127) / 128) * nt < cus;
+    auto go = [&](auto kern, int64_t tm, size_t lds) {
+        const int64_t wgs = ((M + tm - 1) / tm) * nt;
+        if (wgs >= ((int64_t)1 << 31)) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "actq6_mfma: grid too large");
+        int st = allow_dyn_lds(ctx, reinterpret_cast<const void *>(kern), lds, "actq6_mfma: LDS size");
         if (st != TRHIP_OK) return st;
-        hipLaunchKernelGGL(kern, dim3((unsigned)wgs), dim3(Q6_THREADS), Q6L::LDS, ctx->stream, w->planes(), N, row0,
-                           M, w->K, x, q, d, bad, c);
+        hipLaunchKernelGGL(kern, dim3((unsigned)wgs), dim3(Q6_THREADS), lds, ctx->stream, w->planes(), N, row0, M,
+                           w->K, x, q, d, bad, c);
         return launch_check(ctx, "actq6_mfma");
     };
-    return acc ? go(&actq6_mfma<true>) : go(&actq6_mfma<false>);
+    if (small) return acc ? go(&actq6_mfma<true, 4>, 64, Q6L<4>::LDS) : go(&actq6_mfma<false, 4>, 64, Q6L<4>::LDS);
+    return acc ? go(&actq6_mfma<true, 8>, 128, Q6L<8>::LDS) : go(&actq6_mfma<false, 8>, 128, Q6L<8>::LDS);
 }
 
 }  // namespace trhip

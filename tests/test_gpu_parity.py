@@ -397,10 +397,11 @@ def test_actq_tiles_bits(backend, M, N, K, row0, acc):
 
 @pytest.mark.parametrize("M,N,K,row0,acc", [(8, 16, 256, 0, True), (130, 70, 512, 0, False), (257, 129, 1024, 5, True),
                                             (16, 200, 4096, 0, True), (128, 128, 256, 64, False), (300, 1, 512, 0, True),
-                                            (64, 1000, 2048, 3, False)])
+                                            (64, 1000, 2048, 3, False), (130, 16500, 256, 3, True)])
 def test_actq_q6k_tiles_bits(backend, M, N, K, row0, acc):
-    """q6_k act-quant on the int8 matrix cores (128 x 128 tiles, sub-block sums through zero-masked 16x16x64
-    products): row counts that fill, straddle and overhang the tiles, ragged N, a row slice of the store, both
+    """q6_k act-quant on the int8 matrix cores (128 weight rows x 64 or, from 256 workgroups up, 128 activation
+    rows; sub-block sums through zero-masked 16x16x64 products): row counts that fill, straddle and overhang the
+    tiles, ragged N, a row slice of the store, both
     accumulate modes, x1000 / zero / +-1 rows and one NaN row inside a tile, on TR's random-scale blocks (signed
     sub-block scales of every magnitude): bit-identical to quantGemmAct."""
     rng = _rng(M * 5 + N * 3 + K + row0)
