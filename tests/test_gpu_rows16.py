@@ -45,6 +45,25 @@ def test_rows16_shapes(backend, launch_shape, tpw, S, M, N, K, row0):
     w.release()
 
 
+@pytest.mark.parametrize("tpw,S,M,N,K,row0", [(1, 1, 16, 17000, 1024, 3), (2, 4, 11, 9000, 2048, 0),
+                                               (1, 1, 16, 14336, 1024, 0)])
+def test_rows16_pipeline_depths(backend, launch_shape, tpw, S, M, N, K, row0):
+    """The two pipeline depths: grids of more workgroups than a 256-CU device has take three LDS stages (two
+    workgroups per CU), one K slice over at most that many workgroups four: within the tolerance of the oracle."""
+    raw = synth.quant_weights(Q4K, N + row0, K, seed=N + M, outliers=0.01)
+    w = backend.FromQuantized(Q4K, raw, N + row0, K)
+    sub = raw.reshape(N + row0, -1)[row0:].reshape(-1)
+    launch_shape(KNOB_ROWS16, tpw, S)
+    x = synth.activations(M, K, seed=K + M + 5)
+    xb, cb = backend.ctx.to_device(x), backend.ctx.alloc(M * N * 4)
+    backend.GemmSet(M, N, K, xb, w, cb, row0=row0, mode=MODE_FAST)
+    want = O.quant_gemm(Q4K, M, N, K, x, sub).reshape(-1)
+    assert rel_err(cb.download(np.float32, M * N), want) <= FAST_TOL[Q4K]
+    for b in (xb, cb):
+        b.free()
+    w.release()
+
+
 @pytest.mark.parametrize("tpw,S", [(1, 1), (2, 3), (1, 16)])
 @pytest.mark.parametrize("M,I,K", [(16, 300, 4096), (7, 129, 1024)])
 def test_rows16_swiglu_bits(backend, launch_shape, tpw, S, M, I, K):
