@@ -16,9 +16,8 @@
 //
 // Grid: a workgroup is 4 waves over R = 64 TPW weight rows (wave w: TPW tiles of 16 rows; lane l of a tile owns row
 // l % 16 and qs pair g = l / 16, i.e. sub-blocks 2g, 2g + 1) and a K slice of bps blocks. Per block the workgroup
-// brings the block's activation record (written once per call by halves16_kernel) and its rows' headers and qs into
-// LDS by buffer_load ... lds, through three or four stages with one barrier per block, so that two or three blocks
-// are in flight while one is computed. With one slice the results go straight to c; with S > 1 each
+// turns the 16 x 256 activations into the f16 operands in LDS (double-buffered, one barrier per block) while its
+// weights for the next block are in flight. With one slice the results go straight to c; with S > 1 each
 // workgroup writes its slice's partial tile, and the workgroup that arrives last at the row tile's counter adds the
 // S partials in slice order (fixed, so the result does not depend on arrival order) and writes c, then returns the
 // counter to zero. The SwiGLU variant gives a workgroup gate rows i0 .. i0 + R/2 and up rows I + i0 .. so the last
@@ -196,8 +195,7 @@ struct R16Stage {  // one block in LDS: the activation record, the R rows' heade
     static constexpr int DMAS = 5 + 3 * TPW;  // DMA instructions per thread and stage
 };
 
-// NST: LDS stages (3: two workgroups fit on a CU; 4: one, with a block more in flight)
-template <int TPW, bool ACC, bool SWI, int NST>
+template <int TPW, bool ACC, bool SWI>
 __global__ __launch_bounds__(R16_THREADS) void rows16_q4k(const Planes p, int64_t nrows, int64_t N, int64_t row0,
                                                           int64_t M, int64_t K, const float *__restrict__ x,
                                                           const uint8_t *__restrict__ rec, int64_t RT, int S, int bps,
@@ -205,13 +203,11 @@ __global__ __launch_bounds__(R16_THREADS) void rows16_q4k(const Planes p, int64_
                                                           uint32_t *__restrict__ arrivals) {
     using T = R16Stage<TPW>;
     constexpr int R = T::R, H = R / 2;
-    // the stages as separate arrays: the compiler then sees that the reads of one stage do not alias the DMA into
-    // another, and does not wait for the later blocks' loads before computing the current one
-    static_assert(NST == 3 || NST == 4, "three or four stages");
+    // three stages as separate arrays: the compiler then sees that the reads of one stage do not alias the DMA
+    // into another, and does not wait for the later blocks' loads before computing the current one
     __shared__ __align__(16) uint8_t st0[T::BYTES];
     __shared__ __align__(16) uint8_t st1[T::BYTES];
     __shared__ __align__(16) uint8_t st2[T::BYTES];
-    __shared__ __align__(16) uint8_t st3[NST == 4 ? T::BYTES : 16];
     __shared__ int rowbad[16];
     __shared__ int lastflag;
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, n = lane & 15;
@@ -315,41 +311,28 @@ __global__ __launch_bounds__(R16_THREADS) void rows16_q4k(const Planes p, int64_
         }
         if (tid < 16) badrow |= reinterpret_cast<const int *>(cur + R16_BADO)[tid];
     };
-    // Step for block b in stage `cur`: wait until this thread's loads of block b have landed (those of blocks
-    // b + 1 .. b + NST - 2 may still be in flight), barrier (everyone's have; nobody reads the stage of block b - 1
-    // any more), request block b + NST - 1 into that stage, compute block b.
-    // (a plain s_barrier: __syncthreads() would also wait for every load in flight, the next blocks' included)
+    // Step for block b in stage `cur`: wait until this thread's loads of block b have landed (those of the next
+    // block may still be in flight), barrier (everyone's have; nobody reads the stage of block b - 1 any more),
+    // request block b + 2 into that stage, compute block b.
+    // (a plain s_barrier: __syncthreads() would also wait for every load in flight, the next block's included)
     auto step = [&](const uint8_t *cur, uint8_t *nxt, int b) {
-        R16_VMCNT((NST - 2) * T::DMAS);
+        R16_VMCNT(T::DMAS);
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __builtin_amdgcn_s_barrier();
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        stage(nxt, last(b + NST - 1));
+        stage(nxt, last(b + 2));
         compute(cur);
     };
     stage(st0, last(c0));
     stage(st1, last(c0 + 1));
-    int b = c0;  // block c0 + i in stage i % NST
-    if constexpr (NST == 4) {
-        stage(st2, last(c0 + 2));
-        for (; b + 4 <= c1; b += 4) {
-            step(st0, st3, b);
-            step(st1, st0, b + 1);
-            step(st2, st1, b + 2);
-            step(st3, st2, b + 3);
-        }
-        if (b < c1) step(st0, st3, b);
-        if (b + 1 < c1) step(st1, st0, b + 1);
-        if (b + 2 < c1) step(st2, st1, b + 2);
-    } else {
-        for (; b + 3 <= c1; b += 3) {
-            step(st0, st2, b);
-            step(st1, st0, b + 1);
-            step(st2, st1, b + 2);
-        }
-        if (b < c1) step(st0, st2, b);
-        if (b + 1 < c1) step(st1, st0, b + 1);
+    int b = c0;
+    for (; b + 3 <= c1; b += 3) {
+        step(st0, st2, b);
+        step(st1, st0, b + 1);
+        step(st2, st1, b + 2);
     }
+    if (b < c1) step(st0, st2, b);
+    if (b + 1 < c1) step(st1, st0, b + 1);
     R16_VMCNT(0);  // no DMA may still write LDS when the workgroup ends
     if (tid < 16) rowbad[tid] = badrow;
     __syncthreads();
@@ -503,19 +486,19 @@ __global__ __launch_bounds__(R16_THREADS) void rows16_q4k(const Planes p, int64_
     }
 }
 
-template <int TPW, int NST>
+template <int TPW>
 int run_rows16(trhip_ctx *ctx, const Planes &pl, int64_t nrows, int64_t N, int64_t row0, int64_t M, int64_t K,
                const float *x, const uint8_t *rec, int64_t RT, int S, int bps, float *c, float *part, bool acc,
                bool swi) {
     const dim3 grid((unsigned)(RT * S)), block(R16_THREADS);
     if (swi)
-        hipLaunchKernelGGL((rows16_q4k<TPW, false, true, NST>), grid, block, 0, ctx->stream, pl, nrows, N, row0, M, K, x,
+        hipLaunchKernelGGL((rows16_q4k<TPW, false, true>), grid, block, 0, ctx->stream, pl, nrows, N, row0, M, K, x,
                            rec, RT, S, bps, c, part, ctx->arrivals);
     else if (acc)
-        hipLaunchKernelGGL((rows16_q4k<TPW, true, false, NST>), grid, block, 0, ctx->stream, pl, nrows, N, row0, M, K, x,
+        hipLaunchKernelGGL((rows16_q4k<TPW, true, false>), grid, block, 0, ctx->stream, pl, nrows, N, row0, M, K, x,
                            rec, RT, S, bps, c, part, ctx->arrivals);
     else
-        hipLaunchKernelGGL((rows16_q4k<TPW, false, false, NST>), grid, block, 0, ctx->stream, pl, nrows, N, row0, M, K, x,
+        hipLaunchKernelGGL((rows16_q4k<TPW, false, false>), grid, block, 0, ctx->stream, pl, nrows, N, row0, M, K, x,
                            rec, RT, S, bps, c, part, ctx->arrivals);
     return launch_check(ctx, "rows16_q4k");
 }
@@ -570,17 +553,8 @@ int launch_rows16_q4k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64
     float *part = need_part ? reinterpret_cast<float *>(ws + o_p) : nullptr;
     float *dst = fused ? swi : c;
     const Planes pl = w->planes();
-    // four stages for one K slice on a grid that fits on the CUs one workgroup each, else three (two workgroups per
-    // CU). Measured at M = 16, graph replays, three runs interleaved (us, three -> four stages): 14336x4096 (224
-    // workgroups, one slice) 33.0 / 30.1 / 34.6 -> 32.4 / 27.7 / 24.0; with four slices 4096x4096 and 4096x14336
-    // (256 workgroups) 18.6 / 25.4 -> 18.9 / 25.7; more workgroups than CUs, 6144x4096 (288) 20.7 -> 24.8 and the
-    // SwiGLU over 28672x4096 (448) 31.4 -> 38.0
-    const bool deep = S == 1 && RT <= (ctx->sm_count > 0 ? ctx->sm_count : 256);
-    if (tpw == 2)
-        return deep ? run_rows16<2, 4>(ctx, pl, w->N, N, row0, M, K, xa, rec, RT, S, bps, dst, part, acc, fused)
-                    : run_rows16<2, 3>(ctx, pl, w->N, N, row0, M, K, xa, rec, RT, S, bps, dst, part, acc, fused);
-    return deep ? run_rows16<1, 4>(ctx, pl, w->N, N, row0, M, K, xa, rec, RT, S, bps, dst, part, acc, fused)
-                : run_rows16<1, 3>(ctx, pl, w->N, N, row0, M, K, xa, rec, RT, S, bps, dst, part, acc, fused);
+    if (tpw == 2) return run_rows16<2>(ctx, pl, w->N, N, row0, M, K, xa, rec, RT, S, bps, dst, part, acc, fused);
+    return run_rows16<1>(ctx, pl, w->N, N, row0, M, K, xa, rec, RT, S, bps, dst, part, acc, fused);
 }
 
 }  // namespace trhip
