@@ -142,8 +142,8 @@ int trhip_gemm_q(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N,
 
 /* ActQuantGemmer.GemmActQuant (tensor/matmul.go:59-61, tensor/cpu_dtype.go:438-446 ->
  * tensor/cpu_quant_q8.go:125-259): x rows are quantized on the device to Q8 blocks of the
- * weight's block size (quantizeQ8), integer block sums are exact int32 (int8 MFMA for q4_k with
- * M >= 8, packed int8 dot products otherwise), and the per-block
+ * weight's block size (quantizeQ8), integer block sums are exact int32 (int8 MFMA for M >= 8: q4_k, q6_k, and
+ * q4_0 when the row's block count is a multiple of 8; packed int8 dot products otherwise), and the per-block
  * fp32 epilogue follows the reference order, so outputs are bit-identical to the CPU path.
  * Rows holding NaN/Inf use the fp32 path for that row only. dtype must be q4, q4_k or q6_k
  * (QuantActSupported, tensor/cpu_quant_q8.go:122), else TRHIP_ERR_UNSUPPORTED. */
