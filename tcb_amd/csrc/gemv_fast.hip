@@ -293,7 +293,9 @@ struct KlRow<kQ6K> {  // ql pieces t at 32t + 16n, qh pieces at 16t + 8n, the la
 // Slots then alternate gate row i and up row N + i of the same pair; a row's sum does not depend on its slot
 // (lane_sum8 pairs the same lanes for every slot), so the outputs are the unfused GEMV's sums gated exactly as
 // swiglu_kernel gates them.
-template <int DT, bool ACC, int WAVES, int KS, int PD, int RPW, bool SWI = false>
+// SKIP: the grid has more row groups than RPW-row groups need, so a group's last slots may lie past its rows; they
+// still load (a re-read of the last row, which keeps every wait count fixed) but skip the arithmetic
+template <int DT, bool ACC, int WAVES, int KS, int PD, int RPW, bool SWI = false, bool SKIP = false>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const float *__restrict__ x,
                                                       float *__restrict__ c, int64_t N, int64_t row0) {
     static_assert(!(SWI && ACC), "the gated output is set, not accumulated");
@@ -446,7 +448,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const floa
         for (int s = 0; s < 8; s++) {
             const int slot = s % PD;
             const KlRow<DT> rw = R[slot];
-            float a;
+            // (SKIP) a slot past the group's last row skips the arithmetic: its sum is not stored
+            const bool used = !SKIP || (uint32_t)(SWI ? (i0 + s) >> 1 : i0 + s) < nv;  // wave-uniform
+            float a = 0.0f;
+            if (used) {
             if constexpr (DT == kQ6K) {
             const float d6 = f16_to_f32((uint16_t)(rw.d & 0xFFFF));
             const int sh = 4 * (g & 1);  // this lane's nibble and its qh bit pair base
@@ -600,6 +605,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const floa
                 }
             }
             }
+            }
             v[s] = active ? a : 0.0f;
             if (i0 + s + PD < RPW) load_row(R[slot], row_of(i0 + s + PD));  // refill the slot just consumed
         }
@@ -638,20 +644,32 @@ int run_kl(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const
     if (!kl_fits(DT, w->nb, KS)) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv_kl: K parts too long for the lanes of a wave");
     constexpr int OPW = SWI ? RPW / 2 : RPW;  // outputs per row group (SWI: two rows per output)
     int64_t wgs = (N + RG * OPW - 1) / (RG * OPW);  // every row group gets at most RPW rows
-    if (ctx->kl_min_wgs > wgs) wgs = ctx->kl_min_wgs;  // more, shorter row groups (forced for tuning)
+    // Fewer workgroups than CUs: deal the rows over one workgroup per CU (at least one output per row group, the
+    // shorter groups skipping their spare slots) when that leaves each group at most 3/4 of its RPW-row share.
+    // Cold ring, us (same box, interleaved): q6_k 1024x4096 7.70 -> 5.73, q4_0 4096x4096 5.45 -> 4.68, q6_k
+    // 4096x4096 8.02 -> 7.38, q4_k 6144x4096 5.56 -> 5.37 (with SwiGLU 5.63 -> 5.46); not for 14336 rows (16 -> 14
+    // per group): q4_k 8.6 either way, q6_k 13.0 -> 13.3
+    const int64_t cus = ctx->sm_count > 0 ? ctx->sm_count : 256, cap = (N + RG - 1) / RG;
+    const int64_t spread = cus < cap ? cus : cap, per = (N + spread * RG - 1) / (spread * RG);
+    int64_t wide = wgs < cus && 4 * per <= 3 * OPW ? spread : wgs;
+    if (ctx->kl_min_wgs > wide) wide = ctx->kl_min_wgs;  // more, shorter row groups (forced for tuning)
+    const bool skip = wide > wgs;
+    wgs = wide;
     if (N >= (int64_t)1 << 30 || wgs * RG >= (int64_t)1 << 31)
         return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv_kl: more than 2^30 rows");
     dim3 grid((unsigned)wgs), block(64 * WAVES);
-    if constexpr (SWI) {
-        hipLaunchKernelGGL((gemv_kl<DT, false, WAVES, KS, PD, RPW, true>), grid, block, 0, ctx->stream, w->planes(), x, c,
-                           N, row0);
-        return launch_check(ctx, "gemv_kl_swiglu");
-    }
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, block, 0, ctx->stream, w->planes(), x, c, N, row0);
+        return launch_check(ctx, SWI ? "gemv_kl_swiglu" : "gemv_kl");
+    };
+    if constexpr (SWI)
+        return skip ? go(gemv_kl<DT, false, WAVES, KS, PD, RPW, true, true>)
+                    : go(gemv_kl<DT, false, WAVES, KS, PD, RPW, true, false>);
     if (acc)
-        hipLaunchKernelGGL((gemv_kl<DT, true, WAVES, KS, PD, RPW>), grid, block, 0, ctx->stream, w->planes(), x, c, N, row0);
-    else
-        hipLaunchKernelGGL((gemv_kl<DT, false, WAVES, KS, PD, RPW>), grid, block, 0, ctx->stream, w->planes(), x, c, N, row0);
-    return launch_check(ctx, "gemv_kl");
+        return skip ? go(gemv_kl<DT, true, WAVES, KS, PD, RPW, false, true>)
+                    : go(gemv_kl<DT, true, WAVES, KS, PD, RPW, false, false>);
+    return skip ? go(gemv_kl<DT, false, WAVES, KS, PD, RPW, false, true>)
+                : go(gemv_kl<DT, false, WAVES, KS, PD, RPW, false, false>);
 }
 
 template <int D, int WAVES, int KS, int R>
