@@ -780,15 +780,17 @@ int launch_gemv_fast(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_
         if (f != kNotTaken) return f;
         // Measured on cold 1.1 GiB rings (us), K = 4096: 14336 rows 8.6 K across lanes (16 rows per wave) vs
         // 11.6-12.2 row-sliced, 28672 rows 14.7 vs 15.9 with 8 rows per wave; 6144 / 8192 rows 5.6 / 5.8 with 8 rows
-        // per wave vs 7.9 / 8.0 with 16 and 6.2-6.5 / 8.0 row-sliced; at 4096 or fewer rows, or K > 4096, the
-        // row-sliced kernel below is faster.
-        if (N >= 10240 && w->nb >= 8 && w->nb <= 16) return run_kl<kQ4K, 4, 1, 4, 16>(ctx, w, row0, N, x, c, acc);
-        if (N >= 6144 && w->nb >= 8 && w->nb <= 16) return run_kl<kQ4K, 4, 1, 4, 8>(ctx, w, row0, N, x, c, acc);
+        // per wave vs 7.9 / 8.0 with 16 and 6.2-6.5 / 8.0 row-sliced; with the rows of small grids spread over every
+        // CU (run_kl), 4096 / 1024 rows 4.79 / 3.95 vs 4.95 / 4.20 row-sliced. For K > 4096 (K parts) the row-sliced
+        // kernel below is faster (4096x14336: 10.75 vs 11.0-12.9), and below 8 blocks per row lanes would idle.
+        // trhip_set_launch_shape(TRHIP_KNOB_FAST_Q4K) selects the row-sliced kernel.
+        const bool kl_ok = !ctx->force_fast_q4k && w->nb >= 8 && w->nb <= 16;
+        if (kl_ok && N >= 10240) return run_kl<kQ4K, 4, 1, 4, 16>(ctx, w, row0, N, x, c, acc);
+        if (kl_ok) return run_kl<kQ4K, 4, 1, 4, 8>(ctx, w, row0, N, x, c, acc);
         // launch shape "D,WAVES,KS,R": blocks in flight per lane, waves per workgroup, K parts per row group,
         // rows per lane. Measured on cold 1.1 GiB rings: splitting K wins while the grid is small (1024 / 4096 rows
         // at K = 4096: 5.5 / 5.9 us with 2 parts vs 7.9 / 8.2 whole), whole rows per wave win from ~8192 rows
         // (14336 rows: 10.7-11.5 us vs 11.6-11.7). More blocks in flight or more rows per lane were slower.
-        // trhip_set_launch_shape(TRHIP_KNOB_FAST_Q4K) overrides.
         const int forced = ctx->force_fast_q4k;
         // K split in 4 for fewer rows (cold, us): 4096x14336 10.9 vs 14.5 (2 parts), 4096x4096 5.1 vs 6.0,
         // 1024x14336 8.3 vs 12.8
