@@ -218,7 +218,7 @@ int trhip_mfma_probe(trhip_ctx *ctx, int valu_per_mfma, int waves_per_simd, int6
  * (waves, K parts, rows in flight, rows per wave); TRHIP_KNOB_FAST_Q4K: row-sliced fast q4_k GEMV
  * (blocks in flight, waves, K parts, rows per lane); TRHIP_KNOB_EXACT_ROWS: exact four-lane GEMV rows
  * per workgroup a; TRHIP_KNOB_EXACT_LANES: exact GEMV lanes per row a; TRHIP_KNOB_ACTQ_TM: act-quant
- * MFMA row tile a; TRHIP_KNOB_ROWS16: fast q4_k kernel for 2..16 activation rows (a, b) = (16-row tiles per
+ * MFMA row tile a (0: built-in) and, in fast mode, b K slices (0: built-in); TRHIP_KNOB_ROWS16: fast q4_k kernel for 2..16 activation rows (a, b) = (16-row tiles per
  * wave 1 or 2; K slices 1..64, clamped to the block count); TRHIP_KNOB_KL_GRID: at least a workgroups for
  * the K-across-lanes fast GEMV (its rows dealt over more, shorter row groups). */
 enum { TRHIP_KNOB_KL = 1, TRHIP_KNOB_FAST_Q4K = 2, TRHIP_KNOB_EXACT_ROWS = 3, TRHIP_KNOB_EXACT_LANES = 4,

@@ -42,12 +42,17 @@ struct Tile {
 // msum = sum_j S_j m_j with S_j = 64 Sh_j + Sl_j: one f16 MFMA over k = [Sh_0..7 | Sl_0..7] x [64 m_0..7 | m_0..7].
 // Every product and partial sum is an integer below 2^24, so the fp32 result is msum exactly.
 // FAST: the same integer sums with the two products and the accumulation fused (within 1e-4 of the exact result).
+// S > 1 (FAST only): workgroup slice sl of a tile takes blocks [sl bps, sl bps + bps) and writes its partial tile; the
+// workgroup that arrives last at the tile's counter adds the S partials in slice order (so the result does not
+// depend on arrival order), writes c and returns the counter to zero, as rows16.hip does.
 template <bool ACC, int TM, bool FAST>
 __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(TM == 64 ? 2 : 3, TM == 64 ? 2 : 4))) void actq_mfma_q4k(
     const Planes p, int64_t N, int64_t row0, int64_t M, int64_t K, const float *__restrict__ x,
     const int8_t *__restrict__ q, const float *__restrict__ d8, const uint16_t *__restrict__ sj,
-    const uint8_t *__restrict__ bad_blk, float *__restrict__ c) {
+    const uint8_t *__restrict__ bad_blk, float *__restrict__ c, int S, int bps, float *__restrict__ part,
+    uint32_t *__restrict__ arrivals) {
     using T = Tile<TM>;
+    __shared__ int lastflag;
     constexpr int MT = T::MT, ABYTES = T::ABYTES, SBYTES = T::SBYTES, STAGE = T::STAGE, CPW = T::CPW;
     extern __shared__ __align__(16) uint8_t lds[];
     int *rowstate = reinterpret_cast<int *>(lds + 2 * STAGE);  // [TM] 0 ok, 1 NaN/Inf row, 2 outside M
@@ -57,7 +62,11 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(TM == 6
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     int64_t tmi, tni;
-    tile_of(blockIdx.x, (M + TM - 1) / TM, (N + TN - 1) / TN, tmi, tni);
+    const int64_t tiles = ((M + TM - 1) / TM) * ((N + TN - 1) / TN);
+    const int64_t tix = (int64_t)blockIdx.x % tiles;
+    const int sl = (int)((int64_t)blockIdx.x / tiles);
+    const int cb0 = sl * bps, cb1 = cb0 + bps < nb ? cb0 + bps : nb;  // this workgroup's blocks
+    tile_of(tix, (M + TM - 1) / TM, (N + TN - 1) / TN, tmi, tni);
     const int64_t n0 = tni * TN, m0 = tmi * TM;
     tile_row_flags<TM, THREADS>(bad_blk, m0, M, nb, rowstate, anybad);
 
@@ -102,10 +111,10 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(TM == 6
         for (int g = 0; g < 4; g++) wq[g] = qq[8 * b + g];
     };
 
-    fetch_a(0);
-    fetch_w(0);
+    fetch_a(cb0);
+    fetch_w(cb0);
     put_a(0);
-    if (nb > 1) fetch_a(1);
+    if (cb0 + 1 < cb1) fetch_a(cb0 + 1);
     __syncthreads();
 
     float accf[MT][16];
@@ -114,15 +123,15 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(TM == 6
 #pragma unroll
         for (int v = 0; v < 16; v++) accf[t][v] = 0.0f;
 
-    for (int b = 0; b < nb; b++) {
-        const uint8_t *st = lds + (b & 1) * STAGE;
+    for (int b = cb0; b < cb1; b++) {
+        const uint8_t *st = lds + ((b - cb0) & 1) * STAGE;
         // weight block b: scales, then the next block's bytes are requested
         uint32_t sc_lo, sc_hi, m_lo, m_hi;
         q4k_scales(wh.y, wh.z, wh.w, sc_lo, sc_hi, m_lo, m_hi);
         const float dd = f16_to_f32((uint16_t)(wh.x & 0xFFFF)), dm = f16_to_f32((uint16_t)(wh.x >> 16));
         uint4 cq[4] = {wq[0], wq[1], wq[2], wq[3]};
         const uint32_t mlo = m_lo, mhi = m_hi;
-        if (b + 1 < nb) fetch_w(b + 1);
+        if (b + 1 < cb1) fetch_w(b + 1);
 
         v16i c0[MT], c1[MT];
 #pragma unroll
@@ -148,9 +157,9 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(TM == 6
             }
         }
         // stage block b + 1 into the other buffer (last read before the previous barrier), request block b + 2
-        if (b + 1 < nb) {
-            put_a((b + 1) & 1);
-            if (b + 2 < nb) fetch_a(b + 2);
+        if (b + 1 < cb1) {
+            put_a((b + 1 - cb0) & 1);
+            if (b + 2 < cb1) fetch_a(b + 2);
         }
         // msum B operand of this lane's row: [64 m_0..7 | m_0..7] (lanes < 32 hold k 0..7, lanes >= 32 k 8..15)
         const uint32_t mul = (lane >> 5) ? 1u : 64u;
@@ -186,15 +195,48 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(TM == 6
     }
 
     const int64_t gn = n0 + nloc;
+    if (S == 1) {
 #pragma unroll
-    for (int t = 0; t < MT; t++) {
+        for (int t = 0; t < MT; t++) {
 #pragma unroll
-        for (int v = 0; v < 16; v++) {
-            const int mloc = 32 * t + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-            if (gn < N && rowstate[mloc] == 0) {
-                float *o = c + (m0 + mloc) * N + gn;
-                *o = ACC ? *o + accf[t][v] : accf[t][v];
+            for (int v = 0; v < 16; v++) {
+                const int mloc = 32 * t + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                if (gn < N && rowstate[mloc] == 0) {
+                    float *o = c + (m0 + mloc) * N + gn;
+                    *o = ACC ? *o + accf[t][v] : accf[t][v];
+                }
             }
+        }
+    } else {
+        // the slice's partial tile [TM][TN], passed between workgroups as agent-scope atomic stores and loads (the
+        // L2 of each XCD does not hold them back); each thread's stores complete before the workgroup counts in
+        float *pp = part + (tix * S + sl) * (int64_t)(TM * TN);
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int mloc = 32 * t + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                __hip_atomic_store(pp + mloc * TN + nloc, accf[t][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __syncthreads();
+        if (tid == 0)
+            lastflag = __hip_atomic_fetch_add(&arrivals[tix], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                       (uint32_t)(S - 1);
+        __syncthreads();
+        if (!lastflag) return;
+        if (tid == 0) __hip_atomic_store(&arrivals[tix], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const float *p0 = part + tix * S * (int64_t)(TM * TN);
+        for (int i = tid; i < TM * TN; i += THREADS) {
+            const int ml = i / TN, nl = i % TN;
+            if (n0 + nl >= N || rowstate[ml] != 0) continue;
+            float sv = __hip_atomic_load(p0 + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int k = 1; k < S; k++)
+                sv = sv + __hip_atomic_load(p0 + k * (int64_t)(TM * TN) + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            float *o = c + (m0 + ml) * N + (n0 + nl);
+            *o = ACC ? *o + sv : sv;
         }
     }
     // rows holding NaN/Inf take the exact fp32 path (quantGemv) on their own; rare
@@ -213,12 +255,25 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(TM == 6
 
 template <int TM>
 int run_mfma(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c, int64_t M,
-             bool acc, const int8_t *q, const float *d, const uint16_t *sj, const uint8_t *bad, bool fast) {
+             bool acc, const int8_t *q, const float *d, const uint16_t *sj, const uint8_t *bad, bool fast, int S) {
     constexpr size_t lds = Tile<TM>::LDS;
-    dim3 grid((unsigned)(((N + TN - 1) / TN) * ((M + TM - 1) / TM))), block(THREADS);
+    const int64_t tiles = ((N + TN - 1) / TN) * ((M + TM - 1) / TM), nb = w->nb;
+    if (!fast || S < 1) S = 1;  // the exact mode adds the blocks in order
+    if (S > nb) S = (int)nb;
+    const int bps = (int)((nb + S - 1) / S);
+    S = (int)((nb + bps - 1) / bps);
+    float *part = nullptr;
+    if (S > 1) {
+        if (tiles > trhip_ctx::kArrivalSlots || !ctx->arrivals) S = 1;
+        int st = TRHIP_OK;
+        if (S > 1 && !(part = static_cast<float *>(workspace2(ctx, (size_t)(tiles * S * TM * TN) * sizeof(float), &st))))
+            return st;
+    }
+    dim3 grid((unsigned)(tiles * S)), block(THREADS);
     static_assert(lds <= 64 * 1024, "below 64 KB of LDS no launch attribute is needed");
     auto go = [&](auto kern) {
-        hipLaunchKernelGGL(kern, grid, block, lds, ctx->stream, w->planes(), N, row0, M, w->K, x, q, d, sj, bad, c);
+        hipLaunchKernelGGL(kern, grid, block, lds, ctx->stream, w->planes(), N, row0, M, w->K, x, q, d, sj, bad, c, S,
+                           S > 1 ? bps : (int)nb, part, ctx->arrivals);
         return launch_check(ctx, "actq_mfma_q4k");
     };
     if (fast) return acc ? go(&actq_mfma_q4k<true, TM, true>) : go(&actq_mfma_q4k<false, TM, true>);
@@ -999,8 +1054,17 @@ int launch_actq_mfma(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_
     // trhip_set_launch_shape(TRHIP_KNOB_ACTQ_TM) overrides.
     const int64_t wgs64 = ((N + TN - 1) / TN) * ((M + 63) / 64);
     const int tm = ctx->force_actq_tm ? ctx->force_actq_tm : (wgs64 < 160 ? 32 : 64);
-    if (tm == 32) return run_mfma<32>(ctx, w, row0, N, x, c, M, acc, q, d, sj, bad, fast);
-    return run_mfma<64>(ctx, w, row0, N, x, c, M, acc, q, d, sj, bad, fast);
+    // K slices (fast mode): two when K is long (at least 32 blocks) and the tiles fit on the CUs one workgroup each.
+    // Measured (us, one slice -> two): 4096x14336 at M = 128 71.0 -> 52.0, at M = 512 121.5 -> 113.6; with 16
+    // blocks (14336x4096 or 4096x4096 at M = 128) no gain; three or more slices were slower everywhere.
+    // trhip_set_launch_shape(TRHIP_KNOB_ACTQ_TM, tm, S) overrides.
+    int S = ctx->force_actq_slices;
+    if (S == 0 && fast && w->nb >= 32) {
+        const int64_t tiles = ((N + TN - 1) / TN) * ((M + tm - 1) / tm);
+        S = tiles <= (ctx->sm_count > 0 ? ctx->sm_count : 256) ? 2 : 1;
+    }
+    if (tm == 32) return run_mfma<32>(ctx, w, row0, N, x, c, M, acc, q, d, sj, bad, fast, S);
+    return run_mfma<64>(ctx, w, row0, N, x, c, M, acc, q, d, sj, bad, fast, S);
 }
 
 }  // namespace trhip

@@ -425,9 +425,11 @@ int trhip_set_launch_shape(trhip_ctx *ctx, int knob, int a, int b, int c, int d)
         ctx->force_exact_lanes = a;
         return TRHIP_OK;
     case TRHIP_KNOB_ACTQ_TM:
-        if (!(reset || ((a == 32 || a == 64) && !b && !c && !d)))
-            return fail(ctx, TRHIP_ERR_INVALID, "set_launch_shape: act-quant row tile must be 32 or 64");
+        if (!(reset || ((a == 0 || a == 32 || a == 64) && b >= 0 && b <= 64 && !c && !d)))
+            return fail(ctx, TRHIP_ERR_INVALID,
+                        "set_launch_shape: act-quant row tile must be 32 or 64 (0: built-in), K slices 0..64");
         ctx->force_actq_tm = a;
+        ctx->force_actq_slices = b;
         return TRHIP_OK;
     case TRHIP_KNOB_KL_GRID:
         if (!(reset || (a >= 1 && a <= 65536 && !b && !c && !d)))

@@ -227,6 +227,7 @@ struct trhip_ctx {
     int force_exact_rows = 0;   // exact four-lane GEMV rows per workgroup (16, 32, 64)
     int force_exact_lanes = 0;  // exact GEMV lanes per row (4, 8)
     int force_actq_tm = 0;      // act-quant MFMA row tile (32, 64)
+    int force_actq_slices = 0;  // act-quant MFMA K slices, fast mode (0: built-in)
     int force_rows16 = 0;       // batched-decode q4_k kernel: 100 tiles per wave + K slices
     // Arrival counters of kernels whose K slices are summed by the workgroup that finishes a row tile last
     // (rows16.hip): kArrivalSlots zeroed words, each returned to zero by that workgroup.

@@ -13,7 +13,7 @@ import pytest
 import oracle as O
 from conftest import rel_err, same_bits
 from tcb_amd import BLOCK, MODE_EXACT, MODE_FAST, Q4, Q4K, Q6K, Q8, TrhipError
-from tcb_amd._lib import KNOB_KL
+from tcb_amd._lib import KNOB_ACTQ_TM, KNOB_KL
 from tcb_amd import synth
 
 pytestmark = pytest.mark.gpu
@@ -570,7 +570,7 @@ def _run_actq_modes(backend, raw, X, M, N, K, row0, c0, acc):
 @pytest.mark.parametrize("M,N,K,row0,acc", [(8, 64, 256, 0, True), (130, 70, 512, 0, False), (300, 16421, 512, 5, True),
                                             (384, 12800, 1024, 0, False), (128, 14336, 4096, 0, False),
                                             (512, 14336, 4096, 0, False), (512, 4096, 14336, 0, True),
-                                            (2048, 4096, 14336, 0, False)])
+                                            (128, 4096, 14336, 0, True), (2048, 4096, 14336, 0, False)])
 def test_actq_fast_within_tolerance(backend, M, N, K, row0, acc):
     """Fast act-quant (trhip_gemm_q_actq_mode) on encoded model weights: the same quantized activations and exact
     integer block sums with the fp32 epilogue fused, on both matrix-core kernels (64-row tiles below, 128 rows
@@ -601,7 +601,7 @@ def test_actq_fast_within_tolerance(backend, M, N, K, row0, acc):
     assert not np.array_equal(fast[fin].view(np.uint32), want[fin].view(np.uint32))
 
 
-@pytest.mark.parametrize("M,N,K", [(64, 300, 1024), (384, 12800, 1024), (512, 2048, 4096)])
+@pytest.mark.parametrize("M,N,K", [(64, 300, 1024), (384, 12800, 1024), (512, 2048, 4096), (128, 300, 14336)])
 def test_actq_fast_random_scale_blocks(backend, M, N, K):
     """Fast act-quant on TR's random-scale blocks (cpu_quant_test.go:71-86), whose rows cancel: d isum and
     dmin msum nearly cancel inside each block, so any fp32 rounding order of the epilogue lands ulps of the large
@@ -620,6 +620,32 @@ def test_actq_fast_random_scale_blocks(backend, M, N, K):
     truth = xq @ _q4k_weights_f64(raw, N, K).T
     fast_err, exact_err = rel_err(fast, truth), rel_err(exact, truth)
     assert fast_err <= max(1e-4, 2.0 * exact_err), (M, N, K, fast_err, exact_err)
+
+
+@pytest.mark.parametrize("S", [2, 3, 8])
+@pytest.mark.parametrize("tm", [32, 64])
+def test_actq_fast_k_slices(backend, launch_shape, tm, S):
+    """Fast act-quant with K cut into S slices (the last workgroup of a tile adds the partials in slice order):
+    within 1e-4 of quantGemmAct on model weights on ragged tiles with a row slice and accumulation, the same bits
+    on every call, the x1000 row at its input's scale and the NaN row as the exact path computes it."""
+    M, N, K, row0 = 96, 700, 8192, 3
+    launch_shape(KNOB_ACTQ_TM, tm, S)
+    rng = _rng(S + tm)
+    raw = synth.quant_weights(Q4K, row0 + N, K, seed=S + 11, outliers=0.01)
+    X = _x(rng, M * K).reshape(M, K)
+    X[1] *= 1000
+    X[M - 2, 5000] = np.nan
+    c0 = _x(rng, M * N)
+    fast, fast2, exact = _run_actq_modes(backend, raw, X, M, N, K, row0, c0, True)
+    same_bits(fast, fast2)
+    rows = np.ascontiguousarray(raw.reshape(row0 + N, -1)[row0:])
+    want = O.quant_gemm_act(Q4K, M, N, K, X, rows, c0).reshape(M, N)
+    same_bits(exact, want)
+    same_bits(fast[M - 2], want[M - 2])
+    fin = np.ones(M, bool)
+    fin[[1, M - 2]] = False
+    assert rel_err(fast[fin], want[fin]) <= 1e-4
+    assert rel_err(fast[1] / np.float32(1000), want[1] / np.float32(1000)) <= 1e-4
 
 
 @pytest.mark.parametrize("dt", [Q4, Q6K])
