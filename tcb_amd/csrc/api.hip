@@ -777,10 +777,10 @@ int trhip_gemm_q(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N,
         return launch_gemv(ctx, w, row0, N, xa, c, accumulate != 0, mode);
     }
     // fast mode (tolerance) on matrix cores: q4_k from M = 5 (up to 4 rows the exact kernel's 4-row tiles are as
-    // fast), up to 16 rows in one launch over f16 activation pairs, more over fixed-point digits; q6_k from M = 2;
-    // q8_0 / q4_0 run exact (their fast kernel measured slower)
-    if (mode == TRHIP_MODE_FAST && w->dtype == TRHIP_Q4K && M > 4 && M <= 16) {
-        const int r = launch_rows16_q4k(ctx, w, row0, N, x, c, M, accumulate != 0);
+    // fast), up to 16 rows in one launch over f16 activation pairs, more over fixed-point digits; q4_0 up to 16 rows
+    // over f16 activation pairs; q6_k from M = 2; q8_0 and q4_0 beyond 16 rows run exact
+    if (mode == TRHIP_MODE_FAST && M <= 16 && ((w->dtype == TRHIP_Q4K && M > 4) || (w->dtype == TRHIP_Q4 && M > 1))) {
+        const int r = launch_rows16(ctx, w, row0, N, x, c, M, accumulate != 0);
         if (r != -1) return r;
     }
     if (mode == TRHIP_MODE_FAST && ((w->dtype == TRHIP_Q4K && M > 4) || (w->dtype == TRHIP_Q6K && M > 1)))
@@ -817,7 +817,7 @@ int trhip_gemm_q_swiglu(trhip_ctx *ctx, const trhip_wstore *w, const float *x, f
     if (!gu) return st;
     // fast M > 1 on matrix cores (as trhip_gemm_q dispatches it): the gate fused into the K-slice sum
     if (mode == TRHIP_MODE_FAST && K > 0 && w->dtype == TRHIP_Q4K && M > 4 && M <= 16) {
-        const int r = launch_rows16_q4k(ctx, w, 0, w->N, x, nullptr, M, false, out);
+        const int r = launch_rows16(ctx, w, 0, w->N, x, nullptr, M, false, out);
         if (r != -1) return r;
     }
     if (mode == TRHIP_MODE_FAST && K > 0 && ((w->dtype == TRHIP_Q4K && M > 4) || (w->dtype == TRHIP_Q6K && M > 1)))

@@ -1,6 +1,8 @@
-// rows16.hip -- fast-mode (tolerance) q4_k product for 1..16 activation rows in one launch: the batched decode
-// step (c[m, n] (+)= sum_k x[m, k] w[n, k], the reference's quantGemm at small M, tensor/cpu_quant.go:47-147; its
-// GPU twin runs M > 1 as dequantized tiles through a float GEMM, gpu/backend_quant.go:43-134).
+// rows16.hip -- fast-mode (tolerance) q4_k and q4_0 product for 1..16 activation rows in one launch: the batched
+// decode step (c[m, n] (+)= sum_k x[m, k] w[n, k], the reference's quantGemm at small M, tensor/cpu_quant.go:47-147;
+// its GPU twin runs M > 1 as dequantized tiles through a float GEMM, gpu/backend_quant.go:43-134).
+// q4_0 (y = d (q - 8) per 32-element block, tensor/quant.go:149-155) takes the same staging and activation record
+// with one MFMA pair per block: D_b = sum (q - 8)(hi + lo) in fp32, acc += d_b D_b.
 //
 // Arithmetic, per 256-element block b of activation row m (2^E > the block's largest |x|):
 //   x' = x 2^(11-E), held as two f16 terms hi = f16(x'), lo = f16(x' - hi): hi + lo is x' to about 2^-22 of 2^11.
@@ -99,6 +101,9 @@ __device__ __forceinline__ v8h r16_codes(const R16W &r, const R16K &k, int s, ui
 
 // One WG per 256-element block: the 16 x 256 activations as the f16 operand record of the block (hi plane, lo
 // plane, msum operands, exponents, NaN / Inf flags), laid out as the MFMA reads them (step s, lane l at 64 s + l).
+// q4_0 (DT = kQ4): step s is 32-element block s of the 256, and lane group gq holds its elements 4 gq + (0, 2, 1, 3)
+// (the low nibbles of code bytes 4 gq .. 4 gq + 3) and 16 + 4 gq + (0, 2, 1, 3) (their high nibbles); no msum.
+template <int DT>
 __global__ __launch_bounds__(R16_THREADS) void halves16_kernel(const float *__restrict__ x, int64_t M, int64_t K,
                                                                uint8_t *__restrict__ rec) {
     const int b = blockIdx.x, tid = threadIdx.x;
@@ -145,7 +150,9 @@ __global__ __launch_bounds__(R16_THREADS) void halves16_kernel(const float *__re
             hb[i] = __builtin_bit_cast(uint16_t, h);
             lb[i] = __builtin_bit_cast(uint16_t, (_Float16)(a[i] - (float)h));
         }
-        const int slot = (64 * (s0 + jj) + 16 * gq + pm) * 16 + 8 * half;
+        // q4_0: this thread's 16 elements are half pu & 1 of block pu >> 1, elements 4 jj .. 4 jj + 3 of it lane group jj
+        const int slot = DT == kQ4 ? (64 * (pu >> 1) + 16 * jj + pm) * 16 + 8 * (pu & 1)
+                                   : (64 * (s0 + jj) + 16 * gq + pm) * 16 + 8 * half;
         *reinterpret_cast<uint2 *>(st + slot) =
             make_uint2(hb[0] | ((uint32_t)hb[1] << 16), hb[2] | ((uint32_t)hb[3] << 16));
         *reinterpret_cast<uint2 *>(st + R16_PLANE + slot) =
@@ -154,7 +161,7 @@ __global__ __launch_bounds__(R16_THREADS) void halves16_kernel(const float *__re
     const float sum = (((xs[0] + xs[1]) + (xs[2] + xs[3])) + ((xs[4] + xs[5]) + (xs[6] + xs[7]))) +
                       (((xs[8] + xs[9]) + (xs[10] + xs[11])) + ((xs[12] + xs[13]) + (xs[14] + xs[15])));
     const float xsum = (sum + __shfl_xor(sum, 1)) * 0.03125f;  // the 32-element sum / 32: |.| < 2^11
-    if ((pu & 1) == 0) {  // msum A operand: lane (m, kq) holds (hi, lo) of sub-blocks 2 kq, 2 kq + 1
+    if (DT == kQ4K && (pu & 1) == 0) {  // msum A operand: lane (m, kq) holds (hi, lo) of sub-blocks 2 kq, 2 kq + 1
         const _Float16 h = (_Float16)xsum;
         const uint32_t pr = (uint32_t)__builtin_bit_cast(uint16_t, h) |
                             ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(xsum - (float)h)) << 16);
@@ -195,12 +202,15 @@ struct R16Stage {  // one block in LDS: the activation record, the R rows' heade
     static constexpr int DMAS = 5 + 3 * TPW;  // DMA instructions per thread and stage
 };
 
-template <int TPW, bool ACC, bool SWI>
-__global__ __launch_bounds__(R16_THREADS) void rows16_q4k(const Planes p, int64_t nrows, int64_t N, int64_t row0,
-                                                          int64_t M, int64_t K, const float *__restrict__ x,
-                                                          const uint8_t *__restrict__ rec, int64_t RT, int S, int bps,
-                                                          float *__restrict__ c, float *__restrict__ part,
-                                                          uint32_t *__restrict__ arrivals) {
+// DT: q4_k, or q4_0 (its 256-element chunk holds eight blocks: the 16-byte header of a row's chunk is the blocks'
+// eight fp16 scales, its 128 qs bytes their codes, so the staging is the same)
+template <int DT, int TPW, bool ACC, bool SWI>
+__global__ __launch_bounds__(R16_THREADS) void rows16_gemm(const Planes p, int64_t nrows, int64_t N, int64_t row0,
+                                                           int64_t M, int64_t K, const float *__restrict__ x,
+                                                           const uint8_t *__restrict__ rec, int64_t RT, int S, int bps,
+                                                           float *__restrict__ c, float *__restrict__ part,
+                                                           uint32_t *__restrict__ arrivals) {
+    static_assert(DT == kQ4K || (DT == kQ4 && !SWI), "q4_k, or q4_0 without the gate");
     using T = R16Stage<TPW>;
     constexpr int R = T::R, H = R / 2;
     // three stages as separate arrays: the compiler then sees that the reads of one stage do not alias the DMA
@@ -237,7 +247,8 @@ __global__ __launch_bounds__(R16_THREADS) void rows16_q4k(const Planes p, int64_
     // dword 256 i + tid is row / 4, word % 4; the activation record is copied as it is
     const auto rx = r16_rsrc(rec, (uint32_t)(nb * R16_XREC));
     const auto rq = r16_rsrc(p.qs, (uint32_t)(nrows * nb * 128));
-    const auto rh = r16_rsrc(p.aux, (uint32_t)(nrows * nb * 16));
+    const auto rh = r16_rsrc(DT == kQ4 ? static_cast<const void *>(p.d) : static_cast<const void *>(p.aux),
+                             (uint32_t)(nrows * nb * 16));
     uint32_t vq[2 * TPW], vh[TPW];
 #pragma unroll
     for (int i = 0; i < 2 * TPW; i++) {
@@ -270,7 +281,59 @@ __global__ __launch_bounds__(R16_THREADS) void rows16_q4k(const Planes p, int64_
 
     const uint32_t k6464 = opaque(0x64006400u);  // in a register, so the nibble masks fuse into v_and_or_b32
     const v4f zero = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+    auto compute_q4 = [&](const uint8_t *cur) {
+        // q4_0: lane (n, g) of a tile takes code dword g of each block s (low nibbles: elements 4g + (0, 2, 1, 3),
+        // high: 16 + 4g + ...), as exact f16 q - 8 ((1024 + q) - 1032, (1024 + 16 q) / 16 - 72); per block the two
+        // MFMAs give D_s = sum (q - 8)(hi + lo) for the tile, scaled by the row's d_s; per chunk acc += ldexp(., E - 11)
+        R16W cw[TPW];
+        R16K k;
+        k.mul = (h2){(_Float16)1.0f, (_Float16)0.0625f};
+        k.off = (h2){(_Float16)-1032.0f, (_Float16)-72.0f};
+        float ds[TPW][8];
+#pragma unroll
+        for (int tt = 0; tt < TPW; tt++) {
+            const int r = 16 * (TPW * w + tt) + n;
+            uint32_t wd[8];
+#pragma unroll
+            for (int bs = 0; bs < 8; bs++)
+                wd[bs] = *reinterpret_cast<const uint32_t *>(cur + T::QS + 16 * (8 * r + (bs ^ (n & 7))) + 4 * g);
+            cw[tt].a = (u32x4){wd[0], wd[1], wd[2], wd[3]};
+            cw[tt].b = (u32x4){wd[4], wd[5], wd[6], wd[7]};
+            const u32x4 h = *reinterpret_cast<const u32x4 *>(cur + T::HDR + 16 * r);
+#pragma unroll
+            for (int bs = 0; bs < 8; bs++) ds[tt][bs] = f16_to_f32((uint16_t)(h[bs >> 1] >> (16 * (bs & 1))));
+        }
+        float accb[TPW][4];
+#pragma unroll
+        for (int tt = 0; tt < TPW; tt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) accb[tt][r] = 0.0f;
+#pragma unroll
+        for (int bs = 0; bs < 8; bs++) {
+            const v8h ah = reinterpret_cast<const v8h *>(cur)[64 * bs + lane];
+            const v8h al = reinterpret_cast<const v8h *>(cur + R16_PLANE)[64 * bs + lane];
+#pragma unroll
+            for (int tt = 0; tt < TPW; tt++) {
+                const v8h q = r16_codes(cw[tt], k, bs, k6464);
+                v4f Db = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, q, zero, 0, 0, 0);
+                Db = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, q, Db, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; r++) accb[tt][r] = fmaf(ds[tt][bs], Db[r], accb[tt][r]);
+            }
+        }
+        const int4 e4 = reinterpret_cast<const int4 *>(cur + R16_EXO)[g];  // rows 4g .. 4g + 3
+        const int ev[4] = {e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+        for (int tt = 0; tt < TPW; tt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[tt][r] = acc[tt][r] + ldexpf(accb[tt][r], ev[r]);
+        if (tid < 16) badrow |= reinterpret_cast<const int *>(cur + R16_BADO)[tid];
+    };
     auto compute = [&](const uint8_t *cur) {
+        if constexpr (DT == kQ4) {
+            compute_q4(cur);
+            return;
+        }
         R16W cw[TPW];
         R16K k[TPW];
 #pragma unroll
@@ -384,7 +447,7 @@ __global__ __launch_bounds__(R16_THREADS) void rows16_q4k(const Planes p, int64_
                 const int64_t row = row0 + out_row(nl);
                 const float *xr = x + m * K;
                 for (int64_t k = 256 * (int64_t)c0; k < 256 * (int64_t)c1; k += 32)
-                    a = fmaf(xr[k + l32], deq_at<kQ4K>(p, row, k + l32), a);
+                    a = fmaf(xr[k + l32], deq_at<DT>(p, row, k + l32), a);
             }
             float v = a + __shfl_xor(a, 8);
             v = v + __shfl_xor(v, 16);
@@ -486,28 +549,30 @@ __global__ __launch_bounds__(R16_THREADS) void rows16_q4k(const Planes p, int64_
     }
 }
 
-template <int TPW>
+template <int DT, int TPW>
 int run_rows16(trhip_ctx *ctx, const Planes &pl, int64_t nrows, int64_t N, int64_t row0, int64_t M, int64_t K,
                const float *x, const uint8_t *rec, int64_t RT, int S, int bps, float *c, float *part, bool acc,
                bool swi) {
     const dim3 grid((unsigned)(RT * S)), block(R16_THREADS);
     if (swi)
-        hipLaunchKernelGGL((rows16_q4k<TPW, false, true>), grid, block, 0, ctx->stream, pl, nrows, N, row0, M, K, x,
+        hipLaunchKernelGGL((rows16_gemm<kQ4K, TPW, false, true>), grid, block, 0, ctx->stream, pl, nrows, N, row0, M, K, x,
                            rec, RT, S, bps, c, part, ctx->arrivals);
     else if (acc)
-        hipLaunchKernelGGL((rows16_q4k<TPW, true, false>), grid, block, 0, ctx->stream, pl, nrows, N, row0, M, K, x,
+        hipLaunchKernelGGL((rows16_gemm<DT, TPW, true, false>), grid, block, 0, ctx->stream, pl, nrows, N, row0, M, K, x,
                            rec, RT, S, bps, c, part, ctx->arrivals);
     else
-        hipLaunchKernelGGL((rows16_q4k<TPW, false, false>), grid, block, 0, ctx->stream, pl, nrows, N, row0, M, K, x,
+        hipLaunchKernelGGL((rows16_gemm<DT, TPW, false, false>), grid, block, 0, ctx->stream, pl, nrows, N, row0, M, K, x,
                            rec, RT, S, bps, c, part, ctx->arrivals);
-    return launch_check(ctx, "rows16_q4k");
+    return launch_check(ctx, "rows16_gemm");
 }
 
 }  // namespace
 
-int launch_rows16_q4k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
-                      int64_t M, bool acc, float *swi) {
-    if (w->dtype != kQ4K || M < 1 || M > 16 || w->K <= 0 || w->K % 256 != 0) return -1;
+int launch_rows16(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
+                  int64_t M, bool acc, float *swi) {
+    const int dt = w->dtype;
+    if ((dt != kQ4K && dt != kQ4) || M < 1 || M > 16 || w->K <= 0 || w->K % 256 != 0) return -1;
+    if (dt == kQ4 && swi) return -1;  // the gate is fused for q4_k only
     const int64_t K = w->K, nb = K / 256;
     const bool fused = swi != nullptr;
     if (fused && (N % 2 != 0 || acc)) return -1;
@@ -548,13 +613,19 @@ int launch_rows16_q4k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64
         xa = reinterpret_cast<const float *>(ws + o_x);
     }
     uint8_t *rec = ws + o_r;
-    hipLaunchKernelGGL(halves16_kernel, dim3((unsigned)nb), dim3(R16_THREADS), 0, ctx->stream, xa, M, K, rec);
+    if (dt == kQ4)
+        hipLaunchKernelGGL(halves16_kernel<kQ4>, dim3((unsigned)nb), dim3(R16_THREADS), 0, ctx->stream, xa, M, K, rec);
+    else
+        hipLaunchKernelGGL(halves16_kernel<kQ4K>, dim3((unsigned)nb), dim3(R16_THREADS), 0, ctx->stream, xa, M, K, rec);
     if ((st = launch_check(ctx, "halves16")) != TRHIP_OK) return st;
     float *part = need_part ? reinterpret_cast<float *>(ws + o_p) : nullptr;
     float *dst = fused ? swi : c;
     const Planes pl = w->planes();
-    if (tpw == 2) return run_rows16<2>(ctx, pl, w->N, N, row0, M, K, xa, rec, RT, S, bps, dst, part, acc, fused);
-    return run_rows16<1>(ctx, pl, w->N, N, row0, M, K, xa, rec, RT, S, bps, dst, part, acc, fused);
+    if (dt == kQ4)
+        return tpw == 2 ? run_rows16<kQ4, 2>(ctx, pl, w->N, N, row0, M, K, xa, rec, RT, S, bps, dst, part, acc, false)
+                        : run_rows16<kQ4, 1>(ctx, pl, w->N, N, row0, M, K, xa, rec, RT, S, bps, dst, part, acc, false);
+    if (tpw == 2) return run_rows16<kQ4K, 2>(ctx, pl, w->N, N, row0, M, K, xa, rec, RT, S, bps, dst, part, acc, fused);
+    return run_rows16<kQ4K, 1>(ctx, pl, w->N, N, row0, M, K, xa, rec, RT, S, bps, dst, part, acc, fused);
 }
 
 }  // namespace trhip

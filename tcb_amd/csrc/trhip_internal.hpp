@@ -296,7 +296,7 @@ int launch_prefill_q4k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int6
 int launch_mfma_probe(trhip_ctx *ctx, int valu_per_mfma, int waves_per_simd, int64_t iters);
 // Fast-mode q4_k product for 1 <= M <= 16 activation rows in one launch (rows16.hip); swi as in
 // launch_gemm_rows_fast. Returns -1 (nothing launched) where it does not apply.
-int launch_rows16_q4k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
+int launch_rows16(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                       int64_t M, bool acc, float *swi = nullptr);
 // q4_0 and q6_k act-quant on int8 matrix cores (actq4.hip, actq6.hip): whether each takes the shape, and the kernel.
 bool actq4_mfma_applies(int64_t M, int64_t N, int64_t row0, int64_t K);
