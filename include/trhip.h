@@ -134,8 +134,9 @@ int trhip_wstore_to_raw(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int
  * accumulate == 0). mode: TRHIP_MODE_EXACT, or TRHIP_MODE_FAST: deterministic and within 1e-4
  * (q4_k, q6_k) or 1e-5 (q8_0, q4_0) of the exact result, |a - b| / (1 + |b|). Fast mode runs the
  * M == 1 GEMV of every dtype on fixed-point activations (K up to 16384; q8_0 / q4_0 with an even
- * block count), q4_k with M > 4 on int8 matrix cores and q6_k with M > 1 on f16 matrix cores; other
- * cases run exact. The reference GPU's GEMV and its M > 1 dequantize-and-GEMM are tolerance-bound too
+ * block count), q4_k with 5 <= M <= 16 on f16 matrix cores over two-term activations and with M > 16
+ * on int8 matrix cores, q4_0 with 2 <= M <= 16 (K a multiple of 256) and q6_k with M > 1 on f16 matrix
+ * cores; other cases run exact. The reference GPU's GEMV and its M > 1 dequantize-and-GEMM are tolerance-bound too
  * (gpu/kernel_quant_gemv.go:33-84, gpu/backend_quant.go:43-134). */
 int trhip_gemm_q(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x,
                  float *c, int64_t M, int64_t K, int accumulate, int mode);
