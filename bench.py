@@ -39,6 +39,7 @@ Q4K_CODE = 3
 INT8_PEAK_TOPS = 5033.0      # MI355X dense int8 MFMA, datasheet (5.03 POPS)
 N, K = 14336, 4096
 RING_BYTES = int(1.1 * (1 << 30))
+MIN_WARMUP = 1000  # untimed launches of the headline before its timed ones
 COPY_BYTES = 256 << 20
 
 # HBM bytes per launch of the headline kernel from rocprofv3 FETCH_SIZE + WRITE_SIZE over --profile-kernel gemv,
@@ -59,7 +60,9 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400, help="timed GEMVs (rounded up to whole ring passes)")
-    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--warmup", type=int, default=4000,
+                    help="untimed launches before the timed ones (at least %d: with fewer the device is not yet at its "
+                         "steady clock; 72 warm-up launches measured 9.34 us per GEMV, 1008 8.48, 4032 8.28)" % MIN_WARMUP)
     ap.add_argument("--mode", choices=["exact", "fast"], default="fast",
                     help="headline mode; the other mode is measured and reported beside it")
     ap.add_argument("--prefill-m", type=int, default=512)
@@ -480,7 +483,7 @@ def main():
     xb = ctx.to_device(x)
     cb = ctx.alloc(N * 4)
 
-    warm_replays = max(1, -(-a.warmup // ring_n))
+    warm_replays = max(1, -(-max(a.warmup, MIN_WARMUP) // ring_n))
     replays = max(1, -(-a.steps // ring_n))
     steps = replays * ring_n
     abytes = algorithmic_bytes(N, K)
