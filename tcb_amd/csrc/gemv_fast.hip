@@ -218,20 +218,21 @@ __device__ __forceinline__ float lane_sum8(float v[8], int lane) {
 // |X| <= 2^23 * 127/128, split into signed bytes X = d2*2^16 + d1*2^8 + d0 (d0, d1 in [-128, 127], |d2| <= 127).
 // x4_digits packs the digits of four consecutive elements into three dwords (digit t of element k in byte k of
 // dword t); one unit of X weighs 2^(e-23).
+// The digits come from U = X + 0x808080, which lies in [0, 2^24): byte t of U is d_t + 128 (the digits above are
+// the only ones in [-128, 127] with X = d0 + 256 d1 + 65536 d2), so four v_perm_b32 gathers plus one per digit word
+// and an xor of the 0x80 offsets pack them.
 __device__ __forceinline__ void x4_digits(const float *xv, int e, uint32_t out[3]) {
-    uint32_t p0 = 0, p1 = 0, p2 = 0;
+    uint32_t u[4];
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int X = (int)rintf(ldexpf(xv[k], 23 - e));
-        const int d0 = (int)(int8_t)(X & 0xFF), x1 = (X - d0) >> 8;
-        const int d1 = (int)(int8_t)(x1 & 0xFF), d2 = (x1 - d1) >> 8;
-        p0 |= (uint32_t)(d0 & 0xFF) << (8 * k);
-        p1 |= (uint32_t)(d1 & 0xFF) << (8 * k);
-        p2 |= (uint32_t)(d2 & 0xFF) << (8 * k);
-    }
-    out[0] = p0;
-    out[1] = p1;
-    out[2] = p2;
+    for (int k = 0; k < 4; k++) u[k] = (uint32_t)((int)rintf(ldexpf(xv[k], 23 - e)) + 0x808080);
+    // __builtin_amdgcn_perm(s0, s1, sel): byte i of the result is byte sel_i of the eight bytes s1 (0..3), s0 (4..7)
+    const uint32_t a = __builtin_amdgcn_perm(u[1], u[0], 0x05010400u);  // u0.0 u1.0 u0.1 u1.1
+    const uint32_t b = __builtin_amdgcn_perm(u[3], u[2], 0x05010400u);  // u2.0 u3.0 u2.1 u3.1
+    const uint32_t c = __builtin_amdgcn_perm(u[1], u[0], 0x07030602u);  // u0.2 u1.2 u0.3 u1.3
+    const uint32_t d = __builtin_amdgcn_perm(u[3], u[2], 0x07030602u);  // u2.2 u3.2 u2.3 u3.3
+    out[0] = __builtin_amdgcn_perm(b, a, 0x05040100u) ^ 0x80808080u;
+    out[1] = __builtin_amdgcn_perm(b, a, 0x07060302u) ^ 0x80808080u;
+    out[2] = __builtin_amdgcn_perm(d, c, 0x05040100u) ^ 0x80808080u;
 }
 
 // Exponent of a half's grid: m = f * 2^e with f in [0.5, 1) (0 gives e = 0), raised by one when f > 127/128, so
@@ -327,42 +328,43 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const floa
     const int k0 = (2 * g) & 3, k1 = k0 + 1;
     // q4_k: header of the lane's block, and qs 16-byte pieces g and g + 4 of it; q8_0 / q4_0: the two blocks'
     // codes (64 / 32 contiguous bytes) and their two fp16 scales (one aligned dword)
-    const uint4 *hb = reinterpret_cast<const uint4 *>(p.aux) + bc;
-    const uint4 *qb = reinterpret_cast<const uint4 *>(p.qs) +
-                      (K4 ? 8 * (int64_t)bc + g : (DT == kQ8 ? 2 * (int64_t)bc : (int64_t)bc));
-    const uint32_t *db = reinterpret_cast<const uint32_t *>(p.d) + bc / 2;
+    // Loads address a row's planes from a wave-uniform row base (scalar registers) plus a 32-bit byte offset per
+    // lane, which keeps the per-row address arithmetic out of the vector ALU.
     // q6_k: elements 64g .. 64g+63 of the block are 32-element groups k4 = 2 (g & 1) and + 1 of half n = g >> 1;
     // the repacked ql bytes of (t, k4 & 1, l) sit at 32t + 16n + 8 (k4 & 1) + l (low nibbles for k4 < 2), the qh
     // bytes of (t, l) at 16t + 8n + l (bits 2 k4), the scales of the four 16-element quarters at 8n + 4 (g & 1)
     const int n6 = g >> 1;
-    const uint4 *qlb = reinterpret_cast<const uint4 *>(p.qs) + 8 * (int64_t)bc + n6;
-    const uint2 *qhb = reinterpret_cast<const uint2 *>(p.aux) + 8 * (int64_t)bc + n6;
-    const uint32_t *scb = reinterpret_cast<const uint32_t *>(p.sc) + 4 * (int64_t)bc + 2 * n6 + (g & 1);
-    constexpr int QW = K4 ? 8 : (DT == kQ8 ? 2 * 32 / 16 * 2 : 32 / 16);  // uint4 per row in the qs plane / (nb)
+    const uint32_t o_qs = K4 ? 128u * bc + 16u * (DT == kQ4K ? g : n6) : (uint32_t)qs_bytes(DT) * bc;
+    const uint32_t o_aux = DT == kQ4K ? 16u * bc : 64u * bc + 8u * n6;
+    const uint32_t o_sc = 16u * bc + 8u * n6 + 4u * (g & 1);
+    const uint32_t o_d = 2u * bc;  // q8_0 / q4_0 (bc even): the aligned dword of blocks bc, bc + 1
+    auto at = [](const void *base, int64_t off, uint32_t lane_off) {
+        return reinterpret_cast<const uint8_t *>(base) + off + lane_off;
+    };
     auto load_row = [&](KlRow<DT> &rw, int64_t row) {
+        const int64_t rb = row * nb;  // blocks before the row
         if constexpr (DT == kQ4K) {
-            rw.h = hb[row * nb];
-            rw.q0 = qb[row * nb * 8];
-            rw.q1 = qb[row * nb * 8 + 4];
+            rw.h = *reinterpret_cast<const uint4 *>(at(p.aux, rb * 16, o_aux));
+            rw.q0 = *reinterpret_cast<const uint4 *>(at(p.qs, rb * 128, o_qs));
+            rw.q1 = *reinterpret_cast<const uint4 *>(at(p.qs, rb * 128, o_qs + 64));
         } else if constexpr (DT == kQ6K) {
 #pragma unroll
             for (int t = 0; t < 4; t++) {
-                rw.ql[t] = qlb[row * nb * 8 + 2 * t];
-                rw.qh[t] = qhb[row * nb * 8 + 2 * t];
+                rw.ql[t] = *reinterpret_cast<const uint4 *>(at(p.qs, rb * 128, o_qs + 32 * t));
+                rw.qh[t] = *reinterpret_cast<const uint2 *>(at(p.aux, rb * 64, o_aux + 16 * t));
             }
-            rw.sc = scb[row * nb * 4];
-            rw.d = p.d[row * nb + bc];
+            rw.sc = *reinterpret_cast<const uint32_t *>(at(p.sc, rb * 16, o_sc));
+            rw.d = *reinterpret_cast<const uint16_t *>(at(p.d, rb * 2, o_d));
         } else if constexpr (DT == kQ8) {
 #pragma unroll
-            for (int i = 0; i < 4; i++) rw.q[i] = qb[row * nb * 2 + i];
-            rw.d = db[row * (nb / 2)];
+            for (int i = 0; i < 4; i++) rw.q[i] = *reinterpret_cast<const uint4 *>(at(p.qs, rb * 32, o_qs + 16 * i));
+            rw.d = *reinterpret_cast<const uint32_t *>(at(p.d, rb * 2, o_d));
         } else {
-            rw.q0 = qb[row * nb];
-            rw.q1 = qb[row * nb + 1];
-            rw.d = db[row * (nb / 2)];
+            rw.q0 = *reinterpret_cast<const uint4 *>(at(p.qs, rb * 16, o_qs));
+            rw.q1 = *reinterpret_cast<const uint4 *>(at(p.qs, rb * 16, o_qs + 16));
+            rw.d = *reinterpret_cast<const uint32_t *>(at(p.d, rb * 2, o_d));
         }
     };
-    (void)QW;
     // row counts fit 32 bits (the launcher checks), so the uniform row arithmetic stays 32-bit. Without SWI slot i is
     // output row gw + i G; with SWI, slots 2j and 2j + 1 are gate row gw + j G and up row N + gw + j G
     const uint32_t G = gridDim.x * RG, gw = blockIdx.x * RG + rg, n32 = (uint32_t)N;
@@ -386,18 +388,26 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const floa
     int ex[2];  // one unit of X weighs 2^ex (applied last, so subnormal x keeps its value)
     float sxl = 0.0f, sxh = 0.0f;
     {
+        // half (hf) of each column: fixed for RG = 1 (one wave holds all 16 columns); for RG > 1 a wave's CPW <= 8
+        // columns lie in one half, so one running sum and maximum serve and are placed in that half at the end
         float ps[2] = {0.0f, 0.0f}, pm[2] = {0.0f, 0.0f}, xc[CPW * 4];
 #pragma unroll
         for (int i = 0; i < CPW; i++) {
             const float4 t = xraw[i];
             const float e4[4] = {active ? t.x : 0.0f, active ? t.y : 0.0f, active ? t.z : 0.0f, active ? t.w : 0.0f};
-            const int hf = (rg * CPW + i) >> 3;  // wave-uniform
+            const int hf = RG == 1 ? i >> 3 : 0;
 #pragma unroll
             for (int k = 0; k < 4; k++) {
                 xc[4 * i + k] = e4[k];
                 ps[hf] += e4[k];
                 pm[hf] = fmaxf(pm[hf], fabsf(e4[k]));
             }
+        }
+        if (RG > 1 && (rg * CPW) >= 8) {  // wave-uniform
+            ps[1] = ps[0];
+            pm[1] = pm[0];
+            ps[0] = 0.0f;
+            pm[0] = 0.0f;
         }
         xp_lds[part][rg][lane] = make_float4(ps[0], ps[1], pm[0], pm[1]);
         __syncthreads();
@@ -472,9 +482,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const floa
             float pq[4];
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                int l0 = c6[q][0], l1 = c6[q][1], l2 = c6[q][2];
+                const int cw0 = (int)code[q >> 1][4 * (q & 1)];
+                int l0 = sdot4_from(cw0, xd[q >> 1][4 * (q & 1)][0], c6[q][0]);
+                int l1 = sdot4_from(cw0, xd[q >> 1][4 * (q & 1)][1], c6[q][1]);
+                int l2 = sdot4_from(cw0, xd[q >> 1][4 * (q & 1)][2], c6[q][2]);
 #pragma unroll
-                for (int k = 0; k < 4; k++) {
+                for (int k = 1; k < 4; k++) {
                     const int cw = (int)code[q >> 1][4 * (q & 1) + k];
                     l0 = __builtin_amdgcn_sdot4(cw, xd[q >> 1][4 * (q & 1) + k][0], l0, false);
                     l1 = __builtin_amdgcn_sdot4(cw, xd[q >> 1][4 * (q & 1) + k][1], l1, false);
@@ -508,9 +521,18 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const floa
             const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
             const float s0 = d * ubyte_f(scw, k0), n0 = -(dmin * ubyte_f(mw, k0));
             const float s1 = d * ubyte_f(scw, k1), n1 = -(dmin * ubyte_f(mw, k1));
-            int l0 = 0, l1 = 0, l2 = 0, h0 = 0, h1 = 0, h2 = 0;
+            int l0, l1, l2, h0, h1, h2;
+            {
+                const int lo = (int)(qw[0] & 0x0F0F0F0Fu), hi = (int)((qw[0] >> 4) & 0x0F0F0F0Fu);
+                l0 = sdot4_zero(lo, xd[0][0][0]);
+                l1 = sdot4_zero(lo, xd[0][0][1]);
+                l2 = sdot4_zero(lo, xd[0][0][2]);
+                h0 = sdot4_zero(hi, xd[1][0][0]);
+                h1 = sdot4_zero(hi, xd[1][0][1]);
+                h2 = sdot4_zero(hi, xd[1][0][2]);
+            }
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
+            for (int k = 1; k < 8; k++) {
                 const int lo = (int)(qw[k] & 0x0F0F0F0Fu), hi = (int)((qw[k] >> 4) & 0x0F0F0F0Fu);
                 l0 = __builtin_amdgcn_sdot4(lo, xd[0][k][0], l0, false);
                 l1 = __builtin_amdgcn_sdot4(lo, xd[0][k][1], l1, false);
@@ -519,9 +541,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const floa
                 h1 = __builtin_amdgcn_sdot4(hi, xd[1][k][1], h1, false);
                 h2 = __builtin_amdgcn_sdot4(hi, xd[1][k][2], h2, false);
             }
-            // |l1| * 256 + |l0| < 2^24: the first two digits add exactly
-            const float pl = fmaf((float)l2, 65536.0f, fmaf((float)l1, 256.0f, (float)l0));
-            const float ph = fmaf((float)h2, 65536.0f, fmaf((float)h1, 256.0f, (float)h0));
+            // |l1| * 256 + |l0| < 2^24, so the first two digits add exactly, in 32-bit integers as in float
+            const float pl = fmaf((float)l2, 65536.0f, (float)(l1 * 256 + l0));
+            const float ph = fmaf((float)h2, 65536.0f, (float)(h1 * 256 + h0));
             a = ldexpf(s0 * pl, ex[0]);
             a = fmaf(n0, sxl, a);
             a = a + ldexpf(s1 * ph, ex[1]);
@@ -543,7 +565,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const floa
             } else {
             // q8_0: 16 code words, 8 per block; q4_0: 8 words, 4 per block (low nibbles then high nibbles)
             const float d0 = f16_to_f32((uint16_t)(rw.d & 0xFFFF)), d1 = f16_to_f32((uint16_t)(rw.d >> 16));
-            int acc8[2][3] = {{0, 0, 0}, {0, 0, 0}};
+            int acc8[2][3];
             uint32_t qw[16];
             if constexpr (DT == kQ8) {
 #pragma unroll
@@ -559,7 +581,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const floa
                     for (int k = 0; k < 8; k++)
 #pragma unroll
                         for (int t = 0; t < 3; t++)
-                            acc8[hf][t] = __builtin_amdgcn_sdot4((int)qw[8 * hf + k], xd[hf][k][t], acc8[hf][t], false);
+                            acc8[hf][t] = k == 0 ? sdot4_zero((int)qw[8 * hf], xd[hf][0][t])
+                                                 : __builtin_amdgcn_sdot4((int)qw[8 * hf + k], xd[hf][k][t], acc8[hf][t], false);
             } else {
                 const uint32_t w8[8] = {rw.q0.x, rw.q0.y, rw.q0.z, rw.q0.w, rw.q1.x, rw.q1.y, rw.q1.z, rw.q1.w};
 #pragma unroll
@@ -576,7 +599,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const floa
                     for (int k = 0; k < 8; k++)
 #pragma unroll
                         for (int t = 0; t < 3; t++)
-                            acc8[hf][t] = __builtin_amdgcn_sdot4((int)qw[8 * hf + k], xd[hf][k][t], acc8[hf][t], false);
+                            acc8[hf][t] = k == 0 ? sdot4_zero((int)qw[8 * hf], xd[hf][0][t])
+                                                 : __builtin_amdgcn_sdot4((int)qw[8 * hf + k], xd[hf][k][t], acc8[hf][t], false);
             }
             const float pl = fmaf((float)acc8[0][2], 65536.0f, fmaf((float)acc8[0][1], 256.0f, (float)acc8[0][0]));
             const float ph = fmaf((float)acc8[1][2], 65536.0f, fmaf((float)acc8[1][1], 256.0f, (float)acc8[1][0]));

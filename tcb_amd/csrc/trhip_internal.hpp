@@ -72,6 +72,20 @@ __device__ __forceinline__ uint32_t opaque(uint32_t v) {
     return v;
 }
 
+// First v_dot4_i32_i8 of a chain (sum of the four signed byte products plus c) in its three-operand form, whose
+// result register is not the accumulator. __builtin_amdgcn_sdot4 is emitted as the two-operand v_dot4c, which
+// accumulates in place, so a chain started from 0 or from a value still needed later costs a v_mov first.
+__device__ __forceinline__ int sdot4_zero(int a, int b) {
+    int r;
+    asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+__device__ __forceinline__ int sdot4_from(int a, int b, int c) {
+    int r;
+    asm("v_dot4_i32_i8 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
 // Byte k (0..3) of a dword as float: v_cvt_f32_ubyte{k}.
 __device__ __forceinline__ float ubyte_f(uint32_t v, int k) { return (float)((v >> (8 * k)) & 0xFFu); }
 
