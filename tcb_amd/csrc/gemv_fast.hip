@@ -805,12 +805,16 @@ int launch_gemv_fast(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_
         // Measured on cold 1.1 GiB rings (us), K = 4096: 14336 rows 8.6 K across lanes (16 rows per wave) vs
         // 11.6-12.2 row-sliced, 28672 rows 14.7 vs 15.9 with 8 rows per wave; 6144 / 8192 rows 5.6 / 5.8 with 8 rows
         // per wave vs 7.9 / 8.0 with 16 and 6.2-6.5 / 8.0 row-sliced; with the rows of small grids spread over every
-        // CU (run_kl), 4096 / 1024 rows 4.79 / 3.95 vs 4.95 / 4.20 row-sliced. For K > 4096 (K parts) the row-sliced
-        // kernel below is faster (4096x14336: 10.75 vs 11.0-12.9), and below 8 blocks per row lanes would idle.
+        // CU (run_kl), 4096 / 1024 rows 4.79 / 3.95 vs 4.95 / 4.20 row-sliced. Below 8 blocks per row lanes would
+        // idle.
         // trhip_set_launch_shape(TRHIP_KNOB_FAST_Q4K) selects the row-sliced kernel.
         const bool kl_ok = !ctx->force_fast_q4k && w->nb >= 8 && w->nb <= 16;
         if (kl_ok && N >= 10240) return run_kl<kQ4K, 4, 1, 4, 16>(ctx, w, row0, N, x, c, acc);
         if (kl_ok) return run_kl<kQ4K, 4, 1, 4, 8>(ctx, w, row0, N, x, c, acc);
+        // K of 17..64 blocks from 4096 rows: four K parts (4096x14336, cold: 10.25-10.33 us against 10.48-10.66
+        // row-sliced)
+        if (!ctx->force_fast_q4k && w->nb > 16 && kl_fits(kQ4K, w->nb, 4) && N >= 4096)
+            return run_kl<kQ4K, 8, 4, 4, 8>(ctx, w, row0, N, x, c, acc);
         // launch shape "D,WAVES,KS,R": blocks in flight per lane, waves per workgroup, K parts per row group,
         // rows per lane. Measured on cold 1.1 GiB rings: splitting K wins while the grid is small (1024 / 4096 rows
         // at K = 4096: 5.5 / 5.9 us with 2 parts vs 7.9 / 8.2 whole), whole rows per wave win from ~8192 rows
