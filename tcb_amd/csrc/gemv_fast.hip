@@ -669,13 +669,13 @@ int run_kl(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const
     constexpr int OPW = SWI ? RPW / 2 : RPW;  // outputs per row group (SWI: two rows per output)
     int64_t wgs = (N + RG * OPW - 1) / (RG * OPW);  // every row group gets at most RPW rows
     // Fewer workgroups than CUs: deal the rows over one workgroup per CU (at least one output per row group, the
-    // shorter groups skipping their spare slots) when that leaves each group at most 3/4 of its RPW-row share.
-    // Cold ring, us (same box, interleaved): q6_k 1024x4096 7.70 -> 5.73, q4_0 4096x4096 5.45 -> 4.68, q6_k
-    // 4096x4096 8.02 -> 7.38, q4_k 6144x4096 5.56 -> 5.37 (with SwiGLU 5.63 -> 5.46); not for 14336 rows (16 -> 14
-    // per group): q4_k 8.6 either way, q6_k 13.0 -> 13.3
+    // shorter groups skipping their spare slots). Cold ring, us (same box, interleaved): q6_k 1024x4096 7.70 ->
+    // 5.73, q4_0 4096x4096 5.45 -> 4.68, q6_k 4096x4096 8.02 -> 7.38, q4_k 6144x4096 5.56 -> 5.37 (with SwiGLU
+    // 5.63 -> 5.46); at 14336 rows (16 -> 14 rows per group) q4_k 8.03 -> 7.74-7.85, q8_0 12.86 -> 12.55, q6_k
+    // 11.96 -> 11.83, but q4_0 7.64 -> 7.89, so q4_0 spreads only where a group keeps at most 3/4 of its rows.
     const int64_t cus = ctx->sm_count > 0 ? ctx->sm_count : 256, cap = (N + RG - 1) / RG;
     const int64_t spread = cus < cap ? cus : cap, per = (N + spread * RG - 1) / (spread * RG);
-    int64_t wide = wgs < cus && 4 * per <= 3 * OPW ? spread : wgs;
+    int64_t wide = wgs < cus && (DT != kQ4 || 4 * per <= 3 * OPW) ? spread : wgs;
     if (ctx->kl_min_wgs > wide) wide = ctx->kl_min_wgs;  // more, shorter row groups (forced for tuning)
     const bool skip = wide > wgs;
     wgs = wide;
