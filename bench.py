@@ -74,6 +74,8 @@ def parse():
                     default=None,
                     help="run only this kernel --steps times, eagerly (counter runs)")
     ap.add_argument("--rows-m", type=int, default=16, help="activation rows of --profile-kernel rows (M > 1 path)")
+    ap.add_argument("--merged", type=int, default=0,
+                    help="--profile-kernel sweep: 1 = the merged layers ([q | k | v], [gate | up] + SwiGLU) of the bench")
     ap.add_argument("--rows-shape", default="q4_k,14336,4096",
                     help="dtype,N,K of --profile-kernel rows (q4_k or q6_k; e.g. q6_k,128256,4096 for the output head)")
     return ap.parse_args()
@@ -315,13 +317,25 @@ def profile_kernel(a):
         xs = {4096: tb.ctx.to_device(synth.activations(b, 4096, seed=7)),
               14336: tb.ctx.to_device(synth.activations(b, 14336, seed=8))}
         cb = tb.ctx.alloc(b * VOCAB * 4)
+        by = {name: i for i, (name, _, _) in enumerate(LAYER)}
+        if a.merged:  # the bench's merged layers: [q | k | v], o, [gate | up] with the SwiGLU gate, down
+            merged = [(layer[0].Concat([layer[by["q"]], layer[by["k"]], layer[by["v"]]]), layer[by["o"]],
+                       layer[0].Concat([layer[by["gate"]], layer[by["up"]]]), layer[by["down"]]) for layer in stores]
         for _ in range(a.steps):
-            for layer in stores:
-                for (name, n, k), w in zip(LAYER, layer):
-                    tb.GemmSet(b, n, k, xs[k], w, cb, mode=mode)
+            if a.merged:
+                for qkv, o, gu, down in merged:
+                    tb.GemmSet(b, qkv.N, 4096, xs[4096], qkv, cb, mode=mode)
+                    tb.GemmSet(b, 4096, 4096, xs[4096], o, cb, mode=mode)
+                    tb.GemmSwiGLU(b, 4096, xs[4096], gu, cb, mode=mode)
+                    tb.GemmSet(b, 4096, 14336, xs[14336], down, cb, mode=mode)
+            else:
+                for layer in stores:
+                    for (name, n, k), w in zip(LAYER, layer):
+                        tb.GemmSet(b, n, k, xs[k], w, cb, mode=mode)
             tb.GemmSet(b, VOCAB, HIDDEN, xs[4096], head, cb, mode=mode)
         tb.ctx.sync()
-        print(json.dumps({"profiled": "decode_sweep_eager", "batch": b, "mode": a.mode, "token_steps": a.steps}))
+        print(json.dumps({"profiled": "decode_sweep_eager", "batch": b, "mode": a.mode, "token_steps": a.steps,
+                          "merged": bool(a.merged)}))
         tb.close()
         return 0
     raw = synth.quant_weights(Q4K, N, K, seed=3, outliers=0.01)
