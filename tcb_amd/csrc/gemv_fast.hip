@@ -755,9 +755,9 @@ template <int DT>
 int kl_q8q4(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c, bool acc) {
     const int f = kl_forced<DT>(ctx, w, row0, N, x, c, acc);
     if (f != kNotTaken) return f;
-    // cold 1.1 GiB rings (us): q8_0 4096 x 4096 7.2 (one K part) / 6.9 (two), 14336 x 4096 12.7 with 16 rows per
+    // cold 1.1 GiB rings (us): q8_0 4096 x 4096 6.21-6.23 in one K part, 6.38-6.41 in two (with the row arithmetic
+    // of the current kernel; two parts were faster before it, 6.9 against 7.2), 14336 x 4096 12.5 with 16 rows per
     // wave; q4_0 4096 x 4096 5.5 / 6.2, 14336 x 4096 8.2; K = 14336 takes four parts (q8_0 15.0, q4_0 10.7)
-    if (N < 10240 && DT == kQ8 && kl_fits(DT, w->nb, 2)) return run_kl<DT, 4, 2, 4, 8>(ctx, w, row0, N, x, c, acc);
     if (kl_fits(DT, w->nb, 1)) {
         if (N >= 10240) return run_kl<DT, 4, 1, 4, 16>(ctx, w, row0, N, x, c, acc);
         return run_kl<DT, 4, 1, 4, 8>(ctx, w, row0, N, x, c, acc);
