@@ -45,7 +45,7 @@ COPY_BYTES = 256 << 20
 # HBM bytes per launch of the headline kernel from rocprofv3 FETCH_SIZE + WRITE_SIZE over --profile-kernel gemv,
 # each divided by the same counter's reading per byte of the calibration copy (profiles/gemv_q4_k_14336x4096_*.txt).
 # Keyed by mode.
-TRAFFIC = {"fast": 33775279, "exact": 33369237}
+TRAFFIC = {"fast": 33733342, "exact": 33369237}
 # Same counters over --profile-kernel prefill --mode fast (profiles/prefill_q4_k_14336x4096_M512.txt): quantizer +
 # MFMA kernel.
 PREFILL_TRAFFIC = {"quantize_q8": 13295334, "prefill_q4k": 81923421}
