@@ -764,7 +764,8 @@ FAST_TOL = {Q8: 1e-5, Q4: 1e-5, Q4K: 1e-4, Q6K: 1e-4}  # fast-mode bound: 1e-5, 
 
 
 @pytest.mark.parametrize("dt", DTS)
-@pytest.mark.parametrize("N,K", [(7, 256), (64, 512), (130, 2048), (33, 4096), (200, 14336), (1024, 4096)])
+@pytest.mark.parametrize("N,K", [(7, 256), (64, 512), (130, 2048), (33, 4096), (200, 14336), (1024, 4096),
+                                 (14336, 4096), (4096, 14336)])
 def test_gemv_fast_tolerance(backend, dt, N, K):
     """MODE_FAST: |gpu - oracle| / (1 + |oracle|) within the fast-mode bound, for accumulate and set,
     on encoded N(0, 0.02) weights with 1% outliers and on x1000 activations."""
