@@ -448,20 +448,39 @@ int trhip_set_launch_shape(trhip_ctx *ctx, int knob, int a, int b, int c, int d)
 int trhip_check_quant_scales(int dtype, const void *raw, size_t raw_bytes, int64_t *bad_block) {
     if (bad_dtype(dtype) || !bad_block || (raw_bytes && !raw)) return TRHIP_ERR_INVALID;
     const uint8_t *r = static_cast<const uint8_t *>(raw);
-    size_t size = (size_t)block_bytes(dtype);
-    *bad_block = -1;
-    for (size_t b = 0; b * size < raw_bytes; b++) {  // tensor/quant.go:108-128 (a short tail block reads its first bytes)
-        const uint8_t *blk = r + b * size;
-        size_t left = raw_bytes - b * size;
-        bool bad = false;
-        if (dtype == TRHIP_Q8 || dtype == TRHIP_Q4) bad = left >= 2 && bad_scale16(blk);
-        else if (dtype == TRHIP_Q4K) bad = (left >= 2 && bad_scale16(blk)) || (left >= 4 && bad_scale16(blk + 2));
-        else bad = left >= 210 && bad_scale16(blk + 208);
-        if (bad) {
-            *bad_block = (int64_t)b;
-            break;
+    const size_t size = (size_t)block_bytes(dtype), nblk = (raw_bytes + size - 1) / size;
+    // the first block in [b0, b1) whose scale is NaN or Inf, or -1 (tensor/quant.go:108-128; a short tail block
+    // reads its first bytes)
+    auto scan = [=](size_t b0, size_t b1) -> int64_t {
+        for (size_t b = b0; b < b1; b++) {
+            const uint8_t *blk = r + b * size;
+            const size_t left = raw_bytes - b * size;
+            bool bad = false;
+            if (dtype == TRHIP_Q8 || dtype == TRHIP_Q4) bad = left >= 2 && bad_scale16(blk);
+            else if (dtype == TRHIP_Q4K) bad = (left >= 2 && bad_scale16(blk)) || (left >= 4 && bad_scale16(blk + 2));
+            else bad = left >= 210 && bad_scale16(blk + 208);
+            if (bad) return (int64_t)b;
         }
+        return -1;
+    };
+    // Large inputs are scanned in T contiguous ranges by T threads; the first bad block overall is the first one
+    // of the lowest range that has one, the same block the single pass finds.
+    constexpr int T = 8;
+    if (raw_bytes < ((size_t)4 << 20)) {
+        *bad_block = scan(0, nblk);
+        return TRHIP_OK;
     }
+    const size_t part = (nblk + T - 1) / T;
+    int64_t found[T];
+    std::thread th[T - 1];
+    for (int t = 1; t < T; t++) {
+        const size_t b0 = part * t < nblk ? part * t : nblk, b1 = b0 + part < nblk ? b0 + part : nblk;
+        th[t - 1] = std::thread([=, &found] { found[t] = scan(b0, b1); });
+    }
+    found[0] = scan(0, part < nblk ? part : nblk);
+    for (auto &x : th) x.join();
+    *bad_block = -1;
+    for (int t = 0; t < T && *bad_block < 0; t++) *bad_block = found[t];
     return TRHIP_OK;
 }
 
@@ -542,7 +561,7 @@ int upload_ring(trhip_ctx *ctx) {
 
 // memcpy split over a few threads (pageable source -> pinned staging); small copies stay on the calling thread.
 void par_memcpy(void *dst, const void *src, size_t n) {
-    constexpr int T = 4;
+    constexpr int T = 8;
     if (n < ((size_t)4 << 20)) {
         std::memcpy(dst, src, n);
         return;

@@ -68,6 +68,34 @@ def test_check_quant_scales_abi_matches_oracle():
     assert lib.trhip_check_quant_scales(9, None, 0, ctypes.byref(bad)) != 0
 
 
+@pytest.mark.parametrize("dt", [1, 2, 3, 4])
+def test_check_quant_scales_large_inputs(dt):
+    """Inputs of 4 MB and more are scanned in eight contiguous ranges by eight threads: the answer is still the
+    first bad block (the oracle's single pass), with bad blocks in one range, in several, at the range edges, in the
+    last block, and none. A short tail block (not a whole block: the reference's slice of it would panic,
+    quant.go:108-128) has its scale checked only where the scale's bytes lie inside the input."""
+    from tcb_amd import _lib
+    lib = _lib.lib()
+    size = O.BLOCK[dt][1]
+    at = {1: 0, 2: 0, 3: 2, 4: 208}[dt]
+    nblk = (5 << 20) // size + 3
+    part = (nblk + 7) // 8
+    cases = [[], [nblk - 1], [7 * part], [7 * part - 1, 7 * part], [3 * part + 5, 6 * part, part - 1], [0, nblk - 1],
+             [2 * part + 1, 5 * part + 2]]
+    for bads in cases:
+        raw = np.zeros(nblk * size, np.uint8)
+        for b in bads:
+            raw[b * size + at], raw[b * size + at + 1] = 0x00, 0xFC  # -Inf
+        for nbytes in (raw.size, raw.size - size // 2):  # whole blocks, then a short tail block
+            bad = ctypes.c_int64(0)
+            assert lib.trhip_check_quant_scales(dt, raw.ctypes.data_as(ctypes.c_void_p), nbytes, ctypes.byref(bad)) == 0
+            if nbytes == raw.size:
+                assert bad.value == O.check_quant_scales(dt, raw) == (min(bads) if bads else -1), (dt, bads)
+            else:  # the tail's scale counts only if its two bytes are inside the input
+                seen = [x for x in bads if x * size + at + 2 <= nbytes]
+                assert bad.value == (min(seen) if seen else -1), (dt, bads, nbytes)
+
+
 def test_missing_library_fails_loudly(tmp_path):
     from tcb_amd import _lib
     with pytest.raises(ImportError):
