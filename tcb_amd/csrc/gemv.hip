@@ -455,9 +455,10 @@ int launch_exact(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N,
     size_t lds = (size_t)w->K * sizeof(float);
     if (lds > 160 * 1024) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv: K too large for the LDS copy of x");
     // lanes per row: 8 measured faster for q4_k (14336x4096 cold: 15.7 vs 18.0 us; 1024x4096: 12.5 vs 15.9),
-    // q8_0 (4096x4096: 20.3 vs 23.6) and equal for q4_0; 4 stays faster for q6_k (128256x4096: 109 vs 139 us).
-    // trhip_set_launch_shape(TRHIP_KNOB_EXACT_LANES) overrides.
-    const int lanes = ctx->force_exact_lanes ? ctx->force_exact_lanes : (DT == kQ6K ? 4 : 8);
+    // q8_0 (4096x4096: 20.3 vs 23.6) and equal for q4_0; for q6_k 4 stays faster on large grids (14336x4096: 17.8 vs
+    // 19.9 us, 128256x4096: 109 vs 139) and 8 wins below 10240 rows (1024x4096 15.0 -> 10.9, 4096x4096 15.5 -> 11.2,
+    // 4096x14336 47.7 -> 34.5; bit-identical). trhip_set_launch_shape(TRHIP_KNOB_EXACT_LANES) overrides.
+    const int lanes = ctx->force_exact_lanes ? ctx->force_exact_lanes : (DT == kQ6K && N >= 10240 ? 4 : 8);
     if (lanes == 8) {
         // 8 lanes per row: 32 rows per 256-thread workgroup, 16 per 128-thread one and 8 per 64-thread one as N falls
         // (cold, us, 128 -> 64 threads, bit-identical: q4_k 1024x4096 11.0 -> 10.66, 2048x4096 11.1 -> 10.8,
