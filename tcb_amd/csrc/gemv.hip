@@ -462,8 +462,9 @@ int launch_exact(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N,
     if (lanes == 8) {
         // 8 lanes per row: 32 rows per 256-thread workgroup, 16 per 128-thread one and 8 per 64-thread one as N falls
         // (cold, us, 128 -> 64 threads, bit-identical: q4_k 1024x4096 11.0 -> 10.66, 2048x4096 11.1 -> 10.8,
-        // 1024x14336 33.6 -> 32.1; q8_0 / q4_0 1024x4096 18.3 / 18.1 -> 17.9 / 17.2)
-        if (N >= 32 * 200) launch_exact8_t<DT, 256>(ctx, w, row0, N, x, c, acc, lds);
+        // 1024x14336 33.6 -> 32.1; q8_0 / q4_0 1024x4096 18.3 / 18.1 -> 17.9 / 17.2); q4_k keeps 16 rows per workgroup
+        // on large grids too (14336x4096 13.86 -> 13.7, 28672x4096 22.8 -> 22.4; q8_0 / q4_0 lose 1%)
+        if (N >= 32 * 200 && DT != kQ4K) launch_exact8_t<DT, 256>(ctx, w, row0, N, x, c, acc, lds);
         else if (N >= 16 * 200) launch_exact8_t<DT, 128>(ctx, w, row0, N, x, c, acc, lds);
         else launch_exact8_t<DT, 64>(ctx, w, row0, N, x, c, acc, lds);
         return launch_check(ctx, "gemv_exact8");
