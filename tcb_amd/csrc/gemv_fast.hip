@@ -328,8 +328,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const floa
     const int k0 = (2 * g) & 3, k1 = k0 + 1;
     // q4_k: header of the lane's block, and qs 16-byte pieces g and g + 4 of it; q8_0 / q4_0: the two blocks'
     // codes (64 / 32 contiguous bytes) and their two fp16 scales (one aligned dword)
-    // Loads address a row's planes from a wave-uniform row base (scalar registers) plus a 32-bit byte offset per
-    // lane, which keeps the per-row address arithmetic out of the vector ALU.
+    // Loads address a row's planes from a wave-uniform row base plus a fixed 32-bit byte offset per lane, so the
+    // per-row address arithmetic is mostly scalar (two vector adds per row remain, from four).
     // q6_k: elements 64g .. 64g+63 of the block are 32-element groups k4 = 2 (g & 1) and + 1 of half n = g >> 1;
     // the repacked ql bytes of (t, k4 & 1, l) sit at 32t + 16n + 8 (k4 & 1) + l (low nibbles for k4 < 2), the qh
     // bytes of (t, l) at 16t + 8n + l (bits 2 k4), the scales of the four 16-element quarters at 8n + 4 (g & 1)
