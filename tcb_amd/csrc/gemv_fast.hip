@@ -8,7 +8,8 @@
 //
 // Every partial sum is combined in a fixed order inside one workgroup (LDS, then a fixed xor-butterfly),
 // with no atomics, so the result depends only on the shape (the reference forbids atomic accumulation on
-// this path, gpu/kernel_quant_gemv.go:14-16). q4_k only; the other dtypes use the exact kernel.
+// this path, gpu/kernel_quant_gemv.go:14-16). Two kernels: gemv_fast_q4k (row-sliced, q4_k, the paragraphs
+// above) and gemv_kl (K across lanes, fixed-point x on v_dot4, for q4_k, q6_k, q8_0 and q4_0; described below).
 #include "trhip_internal.hpp"
 
 #include <cstdio>
