@@ -58,6 +58,8 @@ int trhip_version(void);
  * gpu/gpu.go:86-170 (Count, setupFn). */
 int trhip_device_count(int *count);
 int trhip_init(int device, trhip_ctx **out);
+/* Destroy order: every weight store and graph made on ctx first, then ctx. While any is alive,
+ * trhip_destroy returns TRHIP_ERR_INVALID and leaves the context (and them) working. */
 int trhip_destroy(trhip_ctx *ctx);
 /* The context's stream as a hipStream_t (for callers that interleave their own work). */
 void *trhip_stream(trhip_ctx *ctx);
@@ -109,11 +111,13 @@ int trhip_check_quant_scales(int dtype, const void *raw, size_t raw_bytes, int64
  * staging (a source inside a trhip_host_alloc block is sent by DMA directly) and repacked on
  * the device into per-field planes (codes, scales) for 128-bit coalesced loads. No value is
  * decoded. A pageable source is copied before the call returns; a pinned one must stay valid
- * until the next trhip_sync on ctx. */
+ * until the next trhip_sync on ctx. The scale gate of trhip_check_quant_scales runs on the host
+ * while earlier chunks are in flight; a bad block (TRHIP_ERR_BAD_SCALE, H6686) drops the store. */
 int trhip_wstore_create(trhip_ctx *ctx, int dtype, const void *raw, size_t raw_bytes, int64_t N,
                         int64_t K, trhip_wstore **out);
 /* Zeroed quantized storage, tensor/quant.go:408-427 (newQuantStorage / QuantZeroRaw): every block
- * byte 0 except the q4 codes, 0x88, so that every element opens to +0. */
+ * byte 0 except the q4 codes, 0x88, so that every element opens to zero: +0 for q8_0, q4_0 and
+ * q4_k, and -0 for q6_k (d*sc*(0-32) with d = +0), as the reference's dequantQ6K gives. */
 int trhip_wstore_create_zero(trhip_ctx *ctx, int dtype, int64_t N, int64_t K, trhip_wstore **out);
 int trhip_wstore_destroy(trhip_wstore *w); /* Releaser.Release, tensor/device.go:520-522 */
 int trhip_wstore_info(const trhip_wstore *w, int *dtype, int64_t *N, int64_t *K, size_t *device_bytes);

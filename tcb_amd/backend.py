@@ -146,9 +146,13 @@ class Context:
         return ms.value
 
     def close(self):
+        """Destroy the context; it is refused (and kept) while stores or graphs made on it are alive."""
         if self.h:
-            _lib.lib().trhip_destroy(self.h)
-            self.h = None
+            code = _lib.lib().trhip_destroy(self.h)
+            if code == _lib.OK:
+                self.h = None
+            return code
+        return _lib.OK
 
 
 class QuantWeight:

@@ -68,15 +68,25 @@ void *workspace2(trhip_ctx *ctx, size_t bytes, int *status) {
     return grow(ctx, ctx->ws2, ctx->ws2_bytes, bytes, status);
 }
 
+// Raise a kernel's dynamic-LDS cap on the context's device to at least `bytes`. The largest size granted so far is
+// kept per (device, kernel): a later call that needs more raises the cap again, one that needs less keeps it.
 int allow_dyn_lds(trhip_ctx *ctx, const void *fn, size_t bytes, const char *what) {
+    struct Grant {
+        int device;
+        const void *fn;
+        size_t bytes;
+    };
     static std::mutex mu;
-    static std::vector<std::pair<int, const void *>> done;
+    static std::vector<Grant> done;
     std::lock_guard<std::mutex> lk(mu);
-    for (const auto &d : done)
-        if (d.first == ctx->device && d.second == fn) return TRHIP_OK;
+    Grant *have = nullptr;
+    for (auto &d : done)
+        if (d.device == ctx->device && d.fn == fn) have = &d;
+    if (have && have->bytes >= bytes) return TRHIP_OK;
     hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
     if (e != hipSuccess) return hip_fail(ctx, e, what);
-    done.emplace_back(ctx->device, fn);
+    if (have) have->bytes = bytes;
+    else done.push_back(Grant{ctx->device, fn, bytes});
     return TRHIP_OK;
 }
 
@@ -145,6 +155,48 @@ size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 int scratch_dev(trhip_ctx *ctx);  // below, beside the static scratch array
 
 bool bad_scale16(const uint8_t *p) { return ((p[0] | (p[1] << 8)) & 0x7C00) == 0x7C00; }
+
+// The first block in [b0, b1) of raw (raw_bytes long) whose fp16 scale is NaN or Inf, or -1
+// (tensor/quant.go:108-128; a short tail block reads its first bytes).
+int64_t scan_scales(int dtype, const uint8_t *r, size_t raw_bytes, size_t b0, size_t b1) {
+    const size_t size = (size_t)block_bytes(dtype);
+    for (size_t b = b0; b < b1; b++) {
+        const uint8_t *blk = r + b * size;
+        const size_t left = raw_bytes - b * size;
+        bool bad = false;
+        if (dtype == TRHIP_Q8 || dtype == TRHIP_Q4) bad = left >= 2 && bad_scale16(blk);
+        else if (dtype == TRHIP_Q4K) bad = (left >= 2 && bad_scale16(blk)) || (left >= 4 && bad_scale16(blk + 2));
+        else bad = left >= 210 && bad_scale16(blk + 208);
+        if (bad) return (int64_t)b;
+    }
+    return -1;
+}
+
+// Host work split over threads: fn(t, lo, hi) for T contiguous ranges [lo, hi) that together cover [0, n).
+// Range 0 runs on the calling thread; a range whose thread cannot be started (std::thread throws on EAGAIN or a
+// process thread limit) runs on the calling thread too, so no exception leaves this function.
+constexpr int kHostThreads = 8;
+template <class F> void for_ranges(size_t n, int T, F &&fn) {
+    if (T < 1) T = 1;
+    if (T > kHostThreads) T = kHostThreads;
+    const size_t part = (n + (size_t)T - 1) / (size_t)T;
+    std::thread th[kHostThreads];
+    for (int t = 1; t < T; t++) {
+        const size_t lo = part * t < n ? part * t : n, hi = lo + part < n ? lo + part : n;
+        if (lo >= hi) continue;
+        try {
+            th[t] = std::thread([&fn, t, lo, hi] { fn(t, lo, hi); });
+        } catch (...) {
+            fn(t, lo, hi);
+        }
+    }
+    fn(0, (size_t)0, part < n ? part : n);
+    for (int t = 1; t < T; t++)
+        if (th[t].joinable()) th[t].join();
+}
+
+// Threads for host passes over `bytes` bytes: one below 4 MiB, where starting threads costs more than it saves.
+int host_threads(size_t bytes) { return bytes < ((size_t)4 << 20) ? 1 : kHostThreads; }
 
 }  // namespace
 
@@ -225,6 +277,11 @@ int trhip_init(int device, trhip_ctx **out) {
 
 int trhip_destroy(trhip_ctx *ctx) {
     if (!ctx) return TRHIP_ERR_INVALID;
+    // Stores and graphs keep using the context's stream (and graphs its retired buffers) until they are destroyed.
+    if (ctx->live_stores > 0 || ctx->live_graphs > 0)
+        return fail(ctx, TRHIP_ERR_INVALID,
+                    "destroy: " + std::to_string(ctx->live_stores) + " weight store(s) and " +
+                        std::to_string(ctx->live_graphs) + " graph(s) of this context are still alive");
     DevGuard g(ctx);
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->ws) (void)hipFree(ctx->ws);
@@ -449,38 +506,14 @@ int trhip_check_quant_scales(int dtype, const void *raw, size_t raw_bytes, int64
     if (bad_dtype(dtype) || !bad_block || (raw_bytes && !raw)) return TRHIP_ERR_INVALID;
     const uint8_t *r = static_cast<const uint8_t *>(raw);
     const size_t size = (size_t)block_bytes(dtype), nblk = (raw_bytes + size - 1) / size;
-    // the first block in [b0, b1) whose scale is NaN or Inf, or -1 (tensor/quant.go:108-128; a short tail block
-    // reads its first bytes)
-    auto scan = [=](size_t b0, size_t b1) -> int64_t {
-        for (size_t b = b0; b < b1; b++) {
-            const uint8_t *blk = r + b * size;
-            const size_t left = raw_bytes - b * size;
-            bool bad = false;
-            if (dtype == TRHIP_Q8 || dtype == TRHIP_Q4) bad = left >= 2 && bad_scale16(blk);
-            else if (dtype == TRHIP_Q4K) bad = (left >= 2 && bad_scale16(blk)) || (left >= 4 && bad_scale16(blk + 2));
-            else bad = left >= 210 && bad_scale16(blk + 208);
-            if (bad) return (int64_t)b;
-        }
-        return -1;
-    };
-    // Large inputs are scanned in T contiguous ranges by T threads; the first bad block overall is the first one
-    // of the lowest range that has one, the same block the single pass finds.
-    constexpr int T = 8;
-    if (raw_bytes < ((size_t)4 << 20)) {
-        *bad_block = scan(0, nblk);
-        return TRHIP_OK;
-    }
-    const size_t part = (nblk + T - 1) / T;
-    int64_t found[T];
-    std::thread th[T - 1];
-    for (int t = 1; t < T; t++) {
-        const size_t b0 = part * t < nblk ? part * t : nblk, b1 = b0 + part < nblk ? b0 + part : nblk;
-        th[t - 1] = std::thread([=, &found] { found[t] = scan(b0, b1); });
-    }
-    found[0] = scan(0, part < nblk ? part : nblk);
-    for (auto &x : th) x.join();
+    // Ranges are scanned in parallel; the first bad block overall is the first one of the lowest range that has
+    // one, the same block a single pass finds.
+    int64_t found[kHostThreads];
+    for (auto &f : found) f = -1;
+    for_ranges(nblk, host_threads(raw_bytes),
+               [&](int t, size_t b0, size_t b1) { found[t] = scan_scales(dtype, r, raw_bytes, b0, b1); });
     *bad_block = -1;
-    for (int t = 0; t < T && *bad_block < 0; t++) *bad_block = found[t];
+    for (int t = 0; t < kHostThreads && *bad_block < 0; t++) *bad_block = found[t];
     return TRHIP_OK;
 }
 
@@ -512,6 +545,7 @@ int new_store(trhip_ctx *ctx, int dtype, int64_t N, int64_t K, trhip_wstore **ou
     w->aux = aux_bytes(dtype) ? w->base + o_aux : nullptr;
     w->sc = sc_bytes(dtype) ? w->base + o_sc : nullptr;
     w->d = d_bytes(dtype) ? reinterpret_cast<uint16_t *>(w->base + o_d) : nullptr;
+    ctx->live_stores++;
     *out = w;
     return TRHIP_OK;
 }
@@ -519,6 +553,7 @@ int new_store(trhip_ctx *ctx, int dtype, int64_t N, int64_t K, trhip_wstore **ou
 void drop_store(trhip_wstore *w) {
     (void)hipStreamSynchronize(w->ctx->stream);
     (void)hipFree(w->base);
+    w->ctx->live_stores--;
     delete w;
 }
 
@@ -534,7 +569,7 @@ bool inside_pinned(const void *p, size_t bytes) {
     return false;
 }
 
-constexpr size_t kUpSlot = (size_t)32 << 20;  // bytes per slot of the upload ring
+constexpr size_t kUpSlot = (size_t)8 << 20;  // bytes per slot of the upload ring (and per upload chunk)
 
 // The context's upload ring: two pinned host buffers and two device staging buffers, made on first use.
 int upload_ring(trhip_ctx *ctx) {
@@ -557,24 +592,6 @@ int upload_ring(trhip_ctx *ctx) {
     }
     ctx->up_slot_bytes = kUpSlot;
     return TRHIP_OK;
-}
-
-// memcpy split over a few threads (pageable source -> pinned staging); small copies stay on the calling thread.
-void par_memcpy(void *dst, const void *src, size_t n) {
-    constexpr int T = 8;
-    if (n < ((size_t)4 << 20)) {
-        std::memcpy(dst, src, n);
-        return;
-    }
-    const size_t part = (n / T + 63) / 64 * 64;
-    std::thread th[T - 1];
-    for (int t = 1; t < T; t++) {
-        const size_t o = part * t;
-        const size_t len = o >= n ? 0 : (n - o < part ? n - o : part);
-        th[t - 1] = std::thread([=] { if (len) std::memcpy(static_cast<char *>(dst) + o, static_cast<const char *>(src) + o, len); });
-    }
-    std::memcpy(dst, src, part < n ? part : n);
-    for (auto &t : th) t.join();
 }
 
 }  // namespace
@@ -623,9 +640,6 @@ int trhip_wstore_create(trhip_ctx *ctx, int dtype, const void *raw, size_t raw_b
     size_t need = (size_t)(N * nb) * (size_t)bb;
     if (raw_bytes != need || (need && !raw))  // H3035
         return fail(ctx, TRHIP_ERR_INVALID, "wstore: raw size does not match N*K");
-    int64_t bad = -1;
-    trhip_check_quant_scales(dtype, raw, raw_bytes, &bad);
-    if (bad >= 0) return fail(ctx, TRHIP_ERR_BAD_SCALE, "wstore: block " + std::to_string(bad) + " has a NaN/Inf scale (H6686)");
     DevGuard g(ctx);
     if (capturing(ctx)) return fail(ctx, TRHIP_ERR_INVALID, "wstore: not allowed while the stream is captured");
     trhip_wstore *w = nullptr;
@@ -635,23 +649,37 @@ int trhip_wstore_create(trhip_ctx *ctx, int dtype, const void *raw, size_t raw_b
         drop_store(w);
         return st;
     }
-    // Chunks of whole blocks (a multiple of 8, so every chunk starts 16-byte aligned in each plane) go through the
-    // two-slot ring: the host copies chunk i into pinned slot i % 2 while the DMA engine uploads chunk i - 1 and the
-    // device repacks it. A source inside a trhip_host_alloc block is uploaded from where it is.
+    // Chunks of whole blocks (a multiple of 8, so every chunk starts 16-byte aligned in each plane) are uploaded
+    // and repacked on the device in stream order. The scale gate (H6686) runs on the host beside the DMA:
+    // - pageable source: the host copies chunk i into pinned slot i % 2 and scans the copied blocks, with
+    //   several threads, while the DMA engine uploads chunk i - 1; a bad block stops before its chunk is sent;
+    // - source inside a trhip_host_alloc block: every chunk is queued from where it is at once, and the whole
+    //   input is scanned while the DMA runs.
+    // Either way the first bad block is the one trhip_check_quant_scales finds, and the store is then dropped.
     const bool pinned = inside_pinned(raw, need);
     const int64_t nblk = N * nb, per = (int64_t)(kUpSlot / (size_t)bb) / 8 * 8;
     const uint8_t *src0 = static_cast<const uint8_t *>(raw);
-    for (int64_t b0 = 0, i = 0; b0 < nblk && st == TRHIP_OK; b0 += per, i++) {
+    int64_t bad = -1;
+    for (int64_t b0 = 0, i = 0; b0 < nblk && st == TRHIP_OK && bad < 0; b0 += per, i++) {
         const int s = (int)(i % trhip_ctx::UP_SLOTS);
         const int64_t nbk = nblk - b0 < per ? nblk - b0 : per;
         const size_t bytes = (size_t)(nbk * bb);
-        const void *src = src0 + (size_t)(b0 * bb);
+        const uint8_t *src = src0 + (size_t)(b0 * bb);
         hipError_t e = hipSuccess;
         if (!pinned) {
             e = hipEventSynchronize(ctx->up_done[s]);  // the slot's previous upload has left it
             if (e == hipSuccess) {
-                par_memcpy(ctx->up_host[s], src, bytes);
-                src = ctx->up_host[s];
+                uint8_t *slot = static_cast<uint8_t *>(ctx->up_host[s]);
+                int64_t found[kHostThreads];
+                for (auto &f : found) f = -1;
+                for_ranges((size_t)nbk, host_threads(bytes), [&](int t, size_t lo, size_t hi) {
+                    std::memcpy(slot + lo * (size_t)bb, src + lo * (size_t)bb, (hi - lo) * (size_t)bb);
+                    found[t] = scan_scales(dtype, slot, bytes, lo, hi);
+                });
+                for (int t = 0; t < kHostThreads && bad < 0; t++)
+                    if (found[t] >= 0) bad = b0 + found[t];
+                if (bad >= 0) break;
+                src = slot;
             }
         }
         if (e == hipSuccess) e = hipMemcpyAsync(ctx->up_dev[s], src, bytes, hipMemcpyHostToDevice, ctx->stream);
@@ -659,6 +687,9 @@ int trhip_wstore_create(trhip_ctx *ctx, int dtype, const void *raw, size_t raw_b
         st = e == hipSuccess ? launch_repack(ctx, w, static_cast<const uint8_t *>(ctx->up_dev[s]), b0, nbk)
                              : hip_fail(ctx, e, "wstore upload");
     }
+    if (st == TRHIP_OK && pinned) trhip_check_quant_scales(dtype, raw, raw_bytes, &bad);
+    if (st == TRHIP_OK && bad >= 0)
+        st = fail(ctx, TRHIP_ERR_BAD_SCALE, "wstore: block " + std::to_string(bad) + " has a NaN/Inf scale (H6686)");
     if (st != TRHIP_OK) {
         drop_store(w);
         return st;
@@ -741,9 +772,7 @@ int trhip_wstore_destroy(trhip_wstore *w) {
     if (!w) return TRHIP_ERR_INVALID;
     DevGuard g(w->ctx);
     if (capturing(w->ctx)) return fail(w->ctx, TRHIP_ERR_INVALID, "wstore_destroy: not allowed while the stream is captured");
-    (void)hipStreamSynchronize(w->ctx->stream);
-    (void)hipFree(w->base);
-    delete w;
+    drop_store(w);
     return TRHIP_OK;
 }
 

@@ -222,6 +222,9 @@ struct trhip_ctx {
     // (or with the context).
     std::vector<void *> retired;
     int live_graphs = 0;
+    // Weight stores of this context not yet destroyed: each holds the context's stream, so the context refuses to
+    // be destroyed before them (and before its graphs).
+    int live_stores = 0;
     // Pinned host staging for host-side index arrays (trhip_embedding_q): reused once the copy that last read it
     // has completed (idx_done).
     void *idx_host = nullptr;
