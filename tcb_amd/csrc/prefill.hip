@@ -66,9 +66,24 @@ __device__ __forceinline__ float pf_epilogue(float acc, int p0, int p1, float cm
     return acc + tt * d8;
 }
 
+// Eight integers below 64 (the bytes of lo, then hi) times c (1 or 64) as f16: v_perm_b32 places each byte under
+// 0x64, giving the f16 value 1024 + v; subtracting 1024 and multiplying by c are both exact (v c <= 4032). (A fused
+// (1024 + v) c - 1024 c is not usable: -1024 * 64 is beyond the f16 range.)
+__device__ __forceinline__ v8h small_f16x8(uint32_t lo, uint32_t hi, _Float16 c) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 cc = (h2){c, c}, off = (h2){(_Float16)(-1024.0f), (_Float16)(-1024.0f)};
+    auto pair = [&](uint32_t v, uint32_t sel) {
+        const h2 x = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, v, sel));
+        return __builtin_bit_cast(uint32_t, (x + off) * cc);
+    };
+    return __builtin_bit_cast(v8h, make_uint4(pair(lo, 0x04010400u), pair(lo, 0x04030402u), pair(hi, 0x04010400u),
+                                              pair(hi, 0x04030402u)));
+}
+
 // One 32-row tile of a block: 16 int8 MFMAs into (c0, c1), and between them the epilogue of the pending tile held in
 // (p0, p1) with msum pcm, the pending block's d, dmin and the d8 of its rows (pd8, this lane's rows at + 8 (v / 4)
-// + (v % 4)): two outputs after each MFMA pair.
+// + (v % 4)). The pending sums are final only once the previous tile's last MFMAs have completed, so the first MFMA
+// pair runs alone and the sixteen outputs follow the next seven pairs (two each, four after the last).
 template <bool FAST>
 __device__ __forceinline__ void pf_tile(v16i &c0, v16i &c1, const v16i &p0, const v16i &p1, const v16f &pcm, float pdd,
                                         float pdm, float *pacc, const float *pd8, const v4i *ar, const v4i (&b0)[8],
@@ -76,33 +91,51 @@ __device__ __forceinline__ void pf_tile(v16i &c0, v16i &c1, const v16i &p0, cons
     c0 = (v16i){0};
     c1 = (v16i){0};
     // LDS reads complete in order, so each is issued a step before it is used and after everything used earlier:
-    // step kc issues d8 of step kc + 1, then A of step kc + 2
+    // step kc issues the d8 of step kc + 1, then A of step kc + 2
     v4i a[3];
     a[0] = ar[0];
-    float2 s8n = *reinterpret_cast<const float2 *>(pd8);
     a[1] = ar[64];
+    float2 s8n = make_float2(0.0f, 0.0f);
+    float4 s8q = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    constexpr int EV = FAST ? 5 : 7;
 #pragma unroll
     for (int kc = 0; kc < 8; kc++) {
         const float2 s8 = s8n;
-        if (kc + 1 < 8) s8n = *reinterpret_cast<const float2 *>(pd8 + 8 * ((kc + 1) >> 1) + 2 * ((kc + 1) & 1));
+        const float4 s8l = s8q;
+        // outputs of step kc: 2 (kc - 1), +1 for kc = 1..6 (d8 pair kc - 1), 12..15 for kc = 7
+        if (kc < 6) s8n = *reinterpret_cast<const float2 *>(pd8 + 8 * (kc >> 1) + 2 * (kc & 1));
+        else if (kc == 6) s8q = *reinterpret_cast<const float4 *>(pd8 + 24);
         if (kc + 2 < 8) a[(kc + 2) % 3] = ar[64 * (kc + 2)];
+        const int nreads = 1 + (kc + 2 < 8);
+        if (nreads == 2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        else __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[kc % 3], b0[kc], c0, 0, 0, 0);
         c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[kc % 3], b1[kc], c1, 0, 0, 0);
-        const float s8v[2] = {s8.x, s8.y};
+        if (kc >= 1 && kc <= 6) {
+            const float s8v[2] = {s8.x, s8.y};
 #pragma unroll
-        for (int r = 0; r < 2; r++) {
-            const int v = 2 * kc + r;
-            pacc[v] = pf_epilogue<FAST>(pacc[v], p0[v], p1[v], pcm[v], pdd, pdm, s8v[r]);
+            for (int r = 0; r < 2; r++) {
+                const int v = 2 * (kc - 1) + r;
+                pacc[v] = pf_epilogue<FAST>(pacc[v], p0[v], p1[v], pcm[v], pdd, pdm, s8v[r]);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, EV, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, EV, 0);
+        } else if (kc == 7) {
+            const float s8v[4] = {s8l.x, s8l.y, s8l.z, s8l.w};
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int v = 12 + r;
+                pacc[v] = pf_epilogue<FAST>(pacc[v], p0[v], p1[v], pcm[v], pdd, pdm, s8v[r]);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 2 * EV, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 2 * EV, 0);
+        } else {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
         }
-        // LDS reads first, then each MFMA followed by one output's epilogue
-        constexpr int EV = FAST ? 5 : 7;
-        const int nreads = (kc + 1 < 8) + (kc + 2 < 8);
-        if (nreads == 2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-        else if (nreads == 1) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, EV, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, EV, 0);
     }
 }
 
@@ -136,43 +169,45 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
     const __amdgpu_buffer_rsrc_t rd = buf_rsrc(dt, (uint32_t)(mpad * nb * 4));
     const __amdgpu_buffer_rsrc_t rwq = buf_rsrc(p.qs, (uint32_t)((row0 + N) * nb * 128));
     const __amdgpu_buffer_rsrc_t rwh = buf_rsrc(p.aux, (uint32_t)((row0 + N) * nb * 16));
-    const uint32_t v16 = 16 * lane;                                                    // activation pieces
-    const uint32_t vd = (uint32_t)((lane >> 5) * nb * 128 + 4 * (lane & 31));         // d8 pieces
-    // weight DMA: codes of 8 rows per instruction, lane j moving 16-byte piece (j % 8) ^ (j / 8) of row j / 8, so
-    // each instruction reads eight whole 128-byte row segments and the LDS slot of piece pc of row r is pc ^ (r % 8)
-    // (conflict-free operand reads); headers by dwords, 16 rows per instruction
+    // weight DMA: codes of 8 rows per instruction, lane j moving a 16-byte piece of row j / 8 to LDS slot j % 8, so
+    // each instruction reads eight whole 128-byte row segments. Slot s of row r holds piece s ^ ((r / 2) % 8): the
+    // 16 rows a b128 operand read pass covers then hit 16 different bank groups (rows are 128 bytes, so rows r and
+    // r + 8 would share banks under a swizzle by r % 8). Headers by dwords, 16 rows per instruction.
     // (rows past row0 + N read zeros from the buffer's bound; their outputs are not stored)
-    const int jr = lane >> 3, jc = lane & 7;
     const int64_t wr0 = row0 + n0 + 32 * w;  // this wave's first weight row
-    const uint32_t vq = (uint32_t)((wr0 + jr) * nb * 128 + 16 * (jc ^ jr));   // + 128 b + 8 q nb 128
-    const uint32_t vh = (uint32_t)((wr0 + (lane >> 2)) * nb * 16 + 4 * (lane & 3));  // + 16 b + 16 q nb 16
+    const uint32_t wq0 = (uint32_t)(wr0 * nb * 128), wh0 = (uint32_t)(wr0 * nb * 16);  // wave-uniform
 
     // stage block b into buffer buf: 1 KB activation pieces i (i < 8 MT codes of tile i / 8, chunk i % 8, then MT
     // msum pieces) dealt round-robin to the waves, the d8 pieces (256 bytes, two tiles each) after them, and each
-    // wave's own weight rows
+    // wave's own weight rows. The per-lane offsets are rebuilt from a lane id the compiler cannot hoist, so no
+    // register holds them across the block's tiles.
     auto stage = [&](int b, int buf) {
+        const uint32_t ln = opaque((uint32_t)lane);
+        const uint32_t v16 = 16 * ln;                                       // activation pieces
+        const uint32_t vd = (ln >> 5) * (uint32_t)nb * 128 + 4 * (ln & 31);  // d8 pieces
+        const uint32_t jr = ln >> 3, jc = ln & 7;
+        // row 8 q + jr of the wave: piece jc ^ (jr / 2) ^ 4 (q % 2)
+        const uint32_t vq0 = jr * (uint32_t)nb * 128 + 16 * (jc ^ (jr >> 1)), vq1 = vq0 ^ 64;
+        const uint32_t vh = (ln >> 2) * (uint32_t)nb * 16 + 4 * (ln & 3);
         uint8_t *sb = lds + buf * STAGE;
         uint8_t *db = lds + T::DOFF + (b % 3) * T::D;
+        // piece i = w + 8 j of the round-robin deal: chunk w of tile j (j < MT), then msum piece w (w < MT), and the
+        // d8 pieces, pieces 9 MT + i, to waves (9 MT + i) % 8 (wave-uniform scalar arithmetic, no branch per piece)
+        static_assert(PF_W == 8 && MT <= PF_W && T::PIECES == 9 * MT, "one chunk per wave and tile");
 #pragma unroll
-        for (int i = 0; i < T::PIECES; i++) {
-            if (i % PF_W != w) continue;
-            if (i < 8 * MT) {
-                const int t = i >> 3, kc = i & 7;
-                BUF_TO_LDS(16, 0, rq, v16, (uint32_t)((((mt0 + t) * nb + b) * 8 + kc) * 1024), sb + 1024 * i);
-            } else {
-                const int t = i - 8 * MT;
-                BUF_TO_LDS(16, 0, rs, v16, (uint32_t)(((mt0 + t) * nb + b) * 1024), sb + T::A + 1024 * t);
-            }
-        }
+        for (int t = 0; t < MT; t++)
+            BUF_TO_LDS(16, 0, rq, v16, (uint32_t)((((mt0 + t) * nb + b) * 8 + w) * 1024), sb + 1024 * (8 * t + w));
+        if (w < MT) BUF_TO_LDS(16, 0, rs, v16, (uint32_t)(((mt0 + w) * nb + b) * 1024), sb + T::A + 1024 * w);
 #pragma unroll
         for (int i = 0; i < MT / 2; i++)
             if ((T::PIECES + i) % PF_W == w)
                 BUF_TO_LDS(4, 0, rd, vd, (uint32_t)(((mt0 + 2 * i) * nb + b) * 128), db + 256 * i);
         uint8_t *wb = sb + T::A + T::S + w * T::WREG;
 #pragma unroll
-        for (int q = 0; q < 2; q++) BUF_TO_LDS(4, 0, rwh, vh, (uint32_t)(16 * b + 256 * q * nb), wb + 256 * q);
+        for (int q = 0; q < 2; q++) BUF_TO_LDS(4, 0, rwh, vh, wh0 + (uint32_t)(16 * b + 256 * q * nb), wb + 256 * q);
 #pragma unroll
-        for (int q = 0; q < 4; q++) BUF_TO_LDS(16, 0, rwq, vq, (uint32_t)(128 * b + 1024 * q * nb), wb + 512 + 1024 * q);
+        for (int q = 0; q < 4; q++)
+            BUF_TO_LDS(16, 0, rwq, (q & 1) ? vq1 : vq0, wq0 + (uint32_t)(128 * b + 1024 * q * nb), wb + 512 + 1024 * q);
     };
 
     stage(0, 0);
@@ -186,7 +221,7 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
     // the first block nothing is pending: zero sums and msum with zero d8 (slot 2, zeroed here) add +-0 to accf =
     // +0, which stays +0.
     v16i x0 = (v16i){0}, x1 = (v16i){0}, y0 = (v16i){0}, y1 = (v16i){0};
-    v16f pcm = (v16f){0.0f};
+    v16f pca = (v16f){0.0f}, pcb = (v16f){0.0f};  // msum of tiles 0, 2 (pca) and 1, 3 (pcb)
     float pdd = 0.0f, pdm = 0.0f;
     if (tid < T::D / 4) reinterpret_cast<float *>(lds + T::DOFF + 2 * T::D)[tid] = 0.0f;
     const int lrow = 4 * (lane >> 5);  // this lane's d8 offset within a tile
@@ -205,9 +240,9 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
         const int ln = (int)opaque((uint32_t)lane), r = ln & 31, h = ln >> 5;
         const uint4 wh = *reinterpret_cast<const uint4 *>(wb + 16 * r);
         uint4 wq[4];  // pieces 4 h + g of row r
-        const uint8_t *wrb = wb + 512 + 1024 * (r >> 3) + 128 * (r & 7);
+        const uint8_t *wrb = wb + 512 + 128 * r;
 #pragma unroll
-        for (int g = 0; g < 4; g++) wq[g] = *reinterpret_cast<const uint4 *>(wrb + 16 * ((4 * h + g) ^ (r & 7)));
+        for (int g = 0; g < 4; g++) wq[g] = *reinterpret_cast<const uint4 *>(wrb + 16 * ((4 * h + g) ^ ((r >> 1) & 7)));
         uint32_t sc_lo, sc_hi, m_lo, m_hi;
         q4k_scales(wh.y, wh.z, wh.w, sc_lo, sc_hi, m_lo, m_hi);
         const float dd = f16_to_f32((uint16_t)(wh.x & 0xFFFF)), dm = f16_to_f32((uint16_t)(wh.x >> 16));
@@ -224,34 +259,32 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
             b1[kc] = mul16(nib, sc >> 3);
         }
         // msum B operand of this lane's row: [64 m_0..7 | m_0..7] (lanes < 32 hold k 0..7, lanes >= 32 k 8..15)
-        const uint32_t mul = (lane >> 5) ? 1u : 64u;
-        const v8h bmv = __builtin_bit_cast(
-            v8h, make_uint4(pack_h2(mul * (m_lo & 0xFF), mul * ((m_lo >> 8) & 0xFF)),
-                            pack_h2(mul * ((m_lo >> 16) & 0xFF), mul * (m_lo >> 24)),
-                            pack_h2(mul * (m_hi & 0xFF), mul * ((m_hi >> 8) & 0xFF)),
-                            pack_h2(mul * ((m_hi >> 16) & 0xFF), mul * (m_hi >> 24))));
+        const v8h bmv = small_f16x8(m_lo, m_hi, (lane >> 5) ? (_Float16)1.0f : (_Float16)64.0f);
 
-        const v4i *ar = reinterpret_cast<const v4i *>(sb) + lane;  // tile t, chunk kc: + 512 t + 64 kc
-        const v8h *am = reinterpret_cast<const v8h *>(sb + T::A) + lane;  // tile t: + 64 t
-        const float *d8b = reinterpret_cast<const float *>(lds + T::DOFF + (b % 3) * T::D) + lrow;
-        const float *d8p = reinterpret_cast<const float *>(lds + T::DOFF + ((b + 2) % 3) * T::D) + lrow;
-        // tiles 0..3 in sets x, y, x, y; each one's epilogue runs inside the next tile
-        pf_tile<FAST>(x0, x1, y0, y1, pcm, pdd, pdm, accf[MT - 1], d8p + 32 * (MT - 1), ar, b0, b1);
-        pcm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[0], bmv, (v16f){0.0f}, 0, 0, 0);
+        // (every LDS address below derives from ln, so none is hoisted out of the loop and held in a register)
+        const v4i *ar = reinterpret_cast<const v4i *>(sb) + ln;  // tile t, chunk kc: + 512 t + 64 kc
+        const v8h *am = reinterpret_cast<const v8h *>(sb + T::A) + ln;  // tile t: + 64 t
+        const float *d8b = reinterpret_cast<const float *>(lds + T::DOFF + (b % 3) * T::D) + 4 * h;
+        const float *d8p = reinterpret_cast<const float *>(lds + T::DOFF + ((b + 2) % 3) * T::D) + 4 * h;
+        // tiles 0..3 in sets x, y, x, y; each one's epilogue runs inside the next tile. A tile's msum MFMA is issued
+        // before its int8 MFMAs, into the msum set the pending epilogue does not read, so it has completed long
+        // before that tile's own epilogue reads it
+        pca = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[0], bmv, (v16f){0.0f}, 0, 0, 0);
+        pf_tile<FAST>(x0, x1, y0, y1, pcb, pdd, pdm, accf[MT - 1], d8p + 32 * (MT - 1), ar, b0, b1);
         pdd = dd;
         pdm = dm;
-        pf_tile<FAST>(y0, y1, x0, x1, pcm, pdd, pdm, accf[0], d8b, ar + 512, b0, b1);
-        pcm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[64], bmv, (v16f){0.0f}, 0, 0, 0);
-        pf_tile<FAST>(x0, x1, y0, y1, pcm, pdd, pdm, accf[1], d8b + 32, ar + 1024, b0, b1);
-        pcm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[128], bmv, (v16f){0.0f}, 0, 0, 0);
-        pf_tile<FAST>(y0, y1, x0, x1, pcm, pdd, pdm, accf[2], d8b + 64, ar + 1536, b0, b1);
-        pcm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[192], bmv, (v16f){0.0f}, 0, 0, 0);
+        pcb = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[64], bmv, (v16f){0.0f}, 0, 0, 0);
+        pf_tile<FAST>(y0, y1, x0, x1, pca, pdd, pdm, accf[0], d8b, ar + 512, b0, b1);
+        pca = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[128], bmv, (v16f){0.0f}, 0, 0, 0);
+        pf_tile<FAST>(x0, x1, y0, y1, pcb, pdd, pdm, accf[1], d8b + 32, ar + 1024, b0, b1);
+        pcb = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[192], bmv, (v16f){0.0f}, 0, 0, 0);
+        pf_tile<FAST>(y0, y1, x0, x1, pca, pdd, pdm, accf[2], d8b + 64, ar + 1536, b0, b1);
     }
-    {  // the last block's last tile (set y)
+    {  // the last block's last tile (set y, msum pcb)
         const float *d8l = reinterpret_cast<const float *>(lds + T::DOFF + ((nb + 2) % 3) * T::D) + lrow + 32 * (MT - 1);
 #pragma unroll
         for (int v = 0; v < 16; v++)
-            accf[MT - 1][v] = pf_epilogue<FAST>(accf[MT - 1][v], y0[v], y1[v], pcm[v], pdd, pdm, d8l[8 * (v >> 2) + (v & 3)]);
+            accf[MT - 1][v] = pf_epilogue<FAST>(accf[MT - 1][v], y0[v], y1[v], pcb[v], pdd, pdm, d8l[8 * (v >> 2) + (v & 3)]);
     }
 
     const int64_t gn = n0 + nloc;
