@@ -45,16 +45,10 @@ struct Pf {
 };
 static_assert(Pf::LDS <= 160 * 1024, "one workgroup per CU");
 
-typedef __attribute__((address_space(3))) void *lds_ptr;
-
-// Raw buffer over [base, base + bytes): per-lane 32-bit offsets, and loads past the end read 0 instead of faulting.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
-}
-// SIZE bytes per lane (16 or 4) from rsrc at voffset + soffset + IMM into LDS at l + IMM + SIZE * lane (l
-// wave-uniform; the immediate offset moves the LDS address too, so offsets that differ per piece go in soffset)
-#define BUF_TO_LDS(SIZE, IMM, r, voffset, soffset, l) \
-    __builtin_amdgcn_raw_ptr_buffer_load_lds((r), (lds_ptr)(l), SIZE, (voffset), (soffset), IMM, 0)
+// The staging copies global memory into LDS with buffer_load ... lds (dma16 / dma4, trhip_internal.hpp), issued as
+// inline assembly: seen by the compiler, such a copy makes it wait for every copy in flight before the block's first
+// LDS read, so the next block's staging would never overlap the current block's work. The kernel waits for its copies
+// itself, once per block, before the barrier.
 
 // The per-block epilogue of one output: exact, in the reference's rounding order (seven VALU), or FAST, the same
 // integer sums with the two products and the accumulation fused (five VALU; within 1e-4 of the exact result).
@@ -164,11 +158,11 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
     // buffers (the launcher checks that every offset fits 32 bits): the tiled activations over rows padded to a
     // multiple of TM, and the store's rows up to row0 + N
     const int64_t mpad = (M + TM - 1) / TM * TM;
-    const __amdgpu_buffer_rsrc_t rq = buf_rsrc(qt, (uint32_t)(mpad * nb * 256));
-    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(st, (uint32_t)(mpad * nb * 32));
-    const __amdgpu_buffer_rsrc_t rd = buf_rsrc(dt, (uint32_t)(mpad * nb * 4));
-    const __amdgpu_buffer_rsrc_t rwq = buf_rsrc(p.qs, (uint32_t)((row0 + N) * nb * 128));
-    const __amdgpu_buffer_rsrc_t rwh = buf_rsrc(p.aux, (uint32_t)((row0 + N) * nb * 16));
+    const dma_rsrc rq = dma_desc(qt, (uint32_t)(mpad * nb * 256));
+    const dma_rsrc rs = dma_desc(st, (uint32_t)(mpad * nb * 32));
+    const dma_rsrc rd = dma_desc(dt, (uint32_t)(mpad * nb * 4));
+    const dma_rsrc rwq = dma_desc(p.qs, (uint32_t)((row0 + N) * nb * 128));
+    const dma_rsrc rwh = dma_desc(p.aux, (uint32_t)((row0 + N) * nb * 16));
     // weight DMA: codes of 8 rows per instruction, lane j moving a 16-byte piece of row j / 8 to LDS slot j % 8, so
     // each instruction reads eight whole 128-byte row segments. Slot s of row r holds piece s ^ ((r / 2) % 8): the
     // 16 rows a b128 operand read pass covers then hit 16 different bank groups (rows are 128 bytes, so rows r and
@@ -196,18 +190,18 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
         static_assert(PF_W == 8 && MT <= PF_W && T::PIECES == 9 * MT, "one chunk per wave and tile");
 #pragma unroll
         for (int t = 0; t < MT; t++)
-            BUF_TO_LDS(16, 0, rq, v16, (uint32_t)((((mt0 + t) * nb + b) * 8 + w) * 1024), sb + 1024 * (8 * t + w));
-        if (w < MT) BUF_TO_LDS(16, 0, rs, v16, (uint32_t)(((mt0 + w) * nb + b) * 1024), sb + T::A + 1024 * w);
+            dma16(rq, lds_addr(sb + 1024 * (8 * t + w)), v16, (uint32_t)((((mt0 + t) * nb + b) * 8 + w) * 1024));
+        if (w < MT) dma16(rs, lds_addr(sb + T::A + 1024 * w), v16, (uint32_t)(((mt0 + w) * nb + b) * 1024));
 #pragma unroll
         for (int i = 0; i < MT / 2; i++)
             if ((T::PIECES + i) % PF_W == w)
-                BUF_TO_LDS(4, 0, rd, vd, (uint32_t)(((mt0 + 2 * i) * nb + b) * 128), db + 256 * i);
+                dma4(rd, lds_addr(db + 256 * i), vd, (uint32_t)(((mt0 + 2 * i) * nb + b) * 128));
         uint8_t *wb = sb + T::A + T::S + w * T::WREG;
 #pragma unroll
-        for (int q = 0; q < 2; q++) BUF_TO_LDS(4, 0, rwh, vh, wh0 + (uint32_t)(16 * b + 256 * q * nb), wb + 256 * q);
+        for (int q = 0; q < 2; q++) dma4(rwh, lds_addr(wb + 256 * q), vh, wh0 + (uint32_t)(16 * b + 256 * q * nb));
 #pragma unroll
         for (int q = 0; q < 4; q++)
-            BUF_TO_LDS(16, 0, rwq, (q & 1) ? vq1 : vq0, wq0 + (uint32_t)(128 * b + 1024 * q * nb), wb + 512 + 1024 * q);
+            dma16(rwq, lds_addr(wb + 512 + 1024 * q), (q & 1) ? vq1 : vq0, wq0 + (uint32_t)(128 * b + 1024 * q * nb));
     };
 
     stage(0, 0);
@@ -229,8 +223,7 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
     for (int b = 0; b < nb; b++) {
         // this wave's loads of block b have landed; after the barrier everyone's have, and nobody reads the other
         // buffer (block b - 1) any more
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
         if (b + 1 < nb) stage(b + 1, (b + 1) & 1);
         const uint8_t *sb = lds + (b & 1) * STAGE;
 

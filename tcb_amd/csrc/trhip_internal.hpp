@@ -72,6 +72,55 @@ __device__ __forceinline__ uint32_t opaque(uint32_t v) {
     return v;
 }
 
+// Global -> LDS copies (buffer_load ... lds) issued as inline assembly. The compiler's waitcnt pass, when it sees
+// an LDS-DMA request in flight, makes every later LDS access it cannot prove disjoint from the request's destination
+// wait for all requests (vmcnt(0)), which turns a prefetch into a stall. Issued this way the requests are invisible
+// to it: the caller waits for them itself with s_waitcnt vmcnt (they complete in issue order), and must not let
+// compiler-visible vector memory loads be outstanding behind them (the compiler's own wait for such a load would
+// count only its loads).
+//
+// Buffer descriptor over [base, base + bytes): per-lane 32-bit offsets; a load past the end reads zeros.
+typedef uint32_t dma_rsrc __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ dma_rsrc dma_desc(const void *base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    return (dma_rsrc){(uint32_t)a, (uint32_t)(a >> 32) & 0xFFFFu, bytes, 0x00020000u};
+}
+// LDS address of a __shared__ pointer (wave-uniform destinations go in M0).
+__device__ __forceinline__ uint32_t lds_addr(const void *p) { return (uint32_t)reinterpret_cast<uintptr_t>(p); }
+// 16 bytes per lane from r at voff + soff into LDS at dst + 16 * lane (dst wave-uniform).
+__device__ __forceinline__ void dma16(dma_rsrc r, uint32_t dst, uint32_t voff, uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(dst), "v"(voff), "s"(r), "s"(soff)
+                 : "memory", "m0");
+}
+// 4 bytes per lane into LDS at dst + 4 * lane.
+__device__ __forceinline__ void dma4(dma_rsrc r, uint32_t dst, uint32_t voff, uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+                 :
+                 : "s"(dst), "v"(voff), "s"(r), "s"(soff)
+                 : "memory", "m0");
+}
+// s_waitcnt vmcnt(n) for n known once the caller's loop is unrolled (the switch folds to one instruction).
+__device__ __forceinline__ void wait_vmcnt(int n) {
+    switch (n) {
+#define TRHIP_VMW(k) \
+    case k: asm volatile("s_waitcnt vmcnt(" #k ")" ::: "memory"); break;
+        TRHIP_VMW(0) TRHIP_VMW(1) TRHIP_VMW(2) TRHIP_VMW(3) TRHIP_VMW(4) TRHIP_VMW(5) TRHIP_VMW(6) TRHIP_VMW(7)
+        TRHIP_VMW(8) TRHIP_VMW(9) TRHIP_VMW(10) TRHIP_VMW(11) TRHIP_VMW(12) TRHIP_VMW(13) TRHIP_VMW(14)
+        TRHIP_VMW(15) TRHIP_VMW(16) TRHIP_VMW(17) TRHIP_VMW(18) TRHIP_VMW(19) TRHIP_VMW(20) TRHIP_VMW(21)
+        TRHIP_VMW(22) TRHIP_VMW(23) TRHIP_VMW(24) TRHIP_VMW(25) TRHIP_VMW(26) TRHIP_VMW(27) TRHIP_VMW(28)
+        TRHIP_VMW(29) TRHIP_VMW(30) TRHIP_VMW(31)
+#undef TRHIP_VMW
+    default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    }
+}
+// Workgroup barrier for data exchanged through LDS: this wave's LDS accesses complete, then s_barrier. (The release
+// fence of __syncthreads also waits for every outstanding vector memory request.)
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // First v_dot4_i32_i8 of a chain (sum of the four signed byte products plus c) in its three-operand form, whose
 // result register is not the accumulator. __builtin_amdgcn_sdot4 is emitted as the two-operand v_dot4c, which
 // accumulates in place, so a chain started from 0 or from a value still needed later costs a v_mov first.
