@@ -39,15 +39,14 @@ struct Q4AL {
 };
 static_assert(Q4AL::LDS <= 80 * 1024, "two workgroups per CU");
 
-typedef __attribute__((address_space(3))) void *q4a_lds_ptr;
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t q4a_rsrc(const void *base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+// Staging copies global memory into LDS with inline-asm buffer_load ... lds (dma16 / dma4, trhip_internal.hpp): a copy
+// the compiler sees makes it wait for every copy in flight before the stage's first LDS read, and the next stage would
+// never overlap the current one's MFMAs. The kernel waits for its copies itself before each stage's barrier.
+__device__ __forceinline__ void q4a_dma16(dma_rsrc r, uint32_t voffset, uint32_t soffset, void *l) {
+    dma16(r, lds_addr(l), voffset, soffset);
 }
-__device__ __forceinline__ void q4a_dma16(__amdgpu_buffer_rsrc_t r, uint32_t voffset, uint32_t soffset, void *l) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (q4a_lds_ptr)l, 16, voffset, soffset, 0, 0);
-}
-__device__ __forceinline__ void q4a_dma4(__amdgpu_buffer_rsrc_t r, uint32_t voffset, uint32_t soffset, void *l) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (q4a_lds_ptr)l, 4, voffset, soffset, 0, 0);
+__device__ __forceinline__ void q4a_dma4(dma_rsrc r, uint32_t voffset, uint32_t soffset, void *l) {
+    dma4(r, lds_addr(l), voffset, soffset);
 }
 
 // Activation piece (row, 16-byte column c of the stage's 256 bytes) at slot 16 row + (c ^ (row & 15)); weight piece
@@ -75,10 +74,10 @@ __global__ __launch_bounds__(Q4A_THREADS) void actq4_mfma(const Planes p, int64_
     tile_row_flags<Q4A_TM, Q4A_THREADS>(bad_blk, m0, M, nb, rowstate, anybad);
 
     // buffers with 32-bit offsets (the launcher checks they fit); reads past the end return 0
-    const __amdgpu_buffer_rsrc_t rq = q4a_rsrc(q, (uint32_t)(M * K));
-    const __amdgpu_buffer_rsrc_t rw = q4a_rsrc(p.qs, (uint32_t)((row0 + N) * nb * 16));
-    const __amdgpu_buffer_rsrc_t rd8 = q4a_rsrc(d8g, (uint32_t)(M * nb * 4));
-    const __amdgpu_buffer_rsrc_t rdw = q4a_rsrc(p.d, (uint32_t)((row0 + N) * nb * 2));
+    const dma_rsrc rq = dma_desc(q, (uint32_t)(M * K));
+    const dma_rsrc rw = dma_desc(p.qs, (uint32_t)((row0 + N) * nb * 16));
+    const dma_rsrc rd8 = dma_desc(d8g, (uint32_t)(M * nb * 4));
+    const dma_rsrc rdw = dma_desc(p.d, (uint32_t)((row0 + N) * nb * 2));
     const int64_t wr0 = row0 + n0;
 
     // DMA offsets per stage s (soffset adds the stage's position). Activation instruction j (16 per stage, four
@@ -126,7 +125,8 @@ __global__ __launch_bounds__(Q4A_THREADS) void actq4_mfma(const Planes p, int64_
 
     stage(0, 0);
     for (int s = 0; s < ns; s++) {
-        __syncthreads();  // stage s has landed (the barrier waits for every load in flight); nobody reads the other
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        // stage s has landed (this wave's copies, then everyone's at the barrier); nobody reads the other
         if (s + 1 < ns) stage(s + 1, (s + 1) & 1);
         const uint8_t *sb = lds + (s & 1) * L::STAGE;
         const float *d8s = reinterpret_cast<const float *>(sb + L::O_D8);

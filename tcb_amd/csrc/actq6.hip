@@ -45,13 +45,11 @@ struct Q6L {
 };
 static_assert(Q6L<8>::LDS <= 160 * 1024, "one workgroup per CU");
 
-typedef __attribute__((address_space(3))) void *q6_lds_ptr;
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t q6_rsrc(const void *base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
-}
-// SIZE bytes per lane from rsrc at voffset + soffset into LDS at l + SIZE * lane (l wave-uniform)
-__device__ __forceinline__ void q6_dma16(__amdgpu_buffer_rsrc_t r, uint32_t voffset, uint32_t soffset, void *l) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (q6_lds_ptr)l, 16, voffset, soffset, 0, 0);
+// Staging copies global memory into LDS with inline-asm buffer_load ... lds (dma16, trhip_internal.hpp): a copy the
+// compiler sees makes it wait for every copy in flight before the block's first LDS read, and the next block's staging
+// would never overlap the current block's MFMAs. The kernel waits for its copies itself before each block's barrier.
+__device__ __forceinline__ void q6_dma16(dma_rsrc r, uint32_t voffset, uint32_t soffset, void *l) {
+    dma16(r, lds_addr(l), voffset, soffset);
 }
 
 // Activation piece (row, 16-byte column c) sits at slot 16 row + (c ^ (row & 7)): the eight rows a quarter-wave
@@ -90,10 +88,10 @@ __global__ __launch_bounds__(Q6_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
     tile_row_flags<Q6_TM, Q6_THREADS>(bad_blk, m0, M, nb, rowstate, anybad);
 
     // buffers with 32-bit offsets (the launcher checks they fit); reads past the end return 0
-    const __amdgpu_buffer_rsrc_t rq = q6_rsrc(q, (uint32_t)(M * K));
-    const __amdgpu_buffer_rsrc_t rql = q6_rsrc(p.qs, (uint32_t)((row0 + N) * nb * 128));
-    const __amdgpu_buffer_rsrc_t rqh = q6_rsrc(p.aux, (uint32_t)((row0 + N) * nb * 64));
-    const __amdgpu_buffer_rsrc_t rsc = q6_rsrc(p.sc, (uint32_t)((row0 + N) * nb * 16));
+    const dma_rsrc rq = dma_desc(q, (uint32_t)(M * K));
+    const dma_rsrc rql = dma_desc(p.qs, (uint32_t)((row0 + N) * nb * 128));
+    const dma_rsrc rqh = dma_desc(p.aux, (uint32_t)((row0 + N) * nb * 64));
+    const dma_rsrc rsc = dma_desc(p.sc, (uint32_t)((row0 + N) * nb * 16));
     const int64_t wr0 = row0 + n0;  // the workgroup's first store row
 
     // DMA offsets. Activation instruction j (TM / 4 per block, TM / 32 per wave): rows 4 j .. 4 j + 3, lane L -> row
@@ -161,7 +159,7 @@ __global__ __launch_bounds__(Q6_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
     for (int b = 0; b < nb; b++) {
         // block b (DMA and scales) is in stage b & 1 once every load has landed; after the barrier nobody reads
         // the other stage (block b - 1) any more
-        __syncthreads();
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
         if (b + 1 < nb) {
             fetch_scales(b + 1);
             stage(b + 1, (b + 1) & 1);
