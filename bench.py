@@ -66,6 +66,8 @@ def parse():
     ap.add_argument("--mode", choices=["exact", "fast"], default="fast",
                     help="headline mode; the other mode is measured and reported beside it")
     ap.add_argument("--prefill-m", type=int, default=512)
+    ap.add_argument("--prefill-dtype", choices=["q4_k", "q6_k", "q4_0"], default="q4_k",
+                    help="weights of --profile-kernel prefill (q6_k and q4_0 take random-code blocks of the same shape)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample (0 = skip)")
     ap.add_argument("--sweep", type=int, default=1, help="also time the 32-layer decode sweep (0 = skip)")
     ap.add_argument("--shapes", type=int, default=1,
@@ -386,15 +388,18 @@ def profile_kernel(a):
         print(json.dumps({"profiled": "open_q_q4_k", "launches": a.steps,
                           "bytes": int(raw.nbytes) + N * K * 4}))
     else:
+        from tcb_amd import Q4, Q6K
         M = a.prefill_m
-        w = tb.FromQuantized(Q4K, raw, N, K)
+        pdt = {"q4_k": Q4K, "q6_k": Q6K, "q4_0": Q4}[a.prefill_dtype]
+        w = tb.FromQuantized(pdt, raw if pdt == Q4K else synth.random_blocks(pdt, N, K, seed=3), N, K)
         Xb = tb.ctx.to_device(synth.activations(M, K, seed=5))
         Cb = tb.ctx.alloc(M * N * 4)
         mode = MODE_FAST if a.mode == "fast" else MODE_EXACT
         for _ in range(a.steps):
             tb.GemmActQuant(M, N, K, Xb, w, Cb, accumulate=False, mode=mode)
         tb.ctx.sync()
-        print(json.dumps({"profiled": "prefill_q4_k_M%d_%s" % (M, a.mode), "launches": a.steps, "ops": 2 * M * N * K}))
+        print(json.dumps({"profiled": "prefill_%s_M%d_%s" % (a.prefill_dtype, M, a.mode), "launches": a.steps,
+                          "ops": 2 * M * N * K}))
     tb.close()
     return 0
 
@@ -571,7 +576,9 @@ def main():
                    "measured_int8_mfma_tops": round(ceiling, 1),
                    "measured_int8_mfma_tops_6valu": round(ceiling7, 1),
                    "frac_of_measured_int8": round(tops / ceiling, 4),
-                   "traffic_bytes": PREFILL_TRAFFIC if M == 512 else None}
+                   "traffic_bytes": PREFILL_TRAFFIC if M == 512 else None,
+                   "traffic_source": "rocprofv3 FETCH_SIZE + WRITE_SIZE over --profile-kernel prefill, kept in "
+                                     "profiles/prefill_q4_k_14336x4096_M512.txt (not measured in this run)"}
         Xb.free()
         Cb.free()
 
@@ -614,6 +621,9 @@ def main():
         "n_gpus": 1,
         "steps": steps,
         "warmup": warm_replays * ring_n,
+        "requested": {"steps": a.steps, "warmup": a.warmup,
+                      "rule": "steps rounded up to whole passes of the %d-copy ring; warm-up at least %d launches" % (
+                          ring_n, MIN_WARMUP)},
         "ms_per_step": round(us_cold / 1e3, 6),
         "higher_is_better": True,
         "scaling": "weak",
@@ -634,6 +644,8 @@ def main():
                                "warm_us_per_gemv": round(us_other_warm, 3)},
         "roofline": {"bound": "hbm", "achieved": round(gbs_cold, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs_cold / HBM_PEAK_GBS, 4), "traffic": TRAFFIC.get(a.mode),
+                     "traffic_source": "rocprofv3 FETCH_SIZE + WRITE_SIZE over --profile-kernel gemv, kept in "
+                                       "profiles/gemv_q4_k_14336x4096_traffic.txt (not measured in this run)",
                      "kernel": "gemv_q4_k_%s" % a.mode, "algorithmic_bytes_per_launch": abytes},
         "prefill": prefill,
         "store_upload": upload,

@@ -20,8 +20,8 @@
 namespace trhip {
 namespace {
 
-// TILED (blk 256, for the prefill MFMA kernel): codes, scales and msum operands go to the tiled layout of
-// prefill.hip (tiled_q / tiled_d / tiled_sj) instead of row-major, and no 16-sums are written.
+// TILED (blk 256, for the prefill MFMA kernels): codes, scales and (q4_k, sj not null) msum operands go to the tiled
+// layout of prefill.hip (tiled_q / tiled_d / tiled_sj) instead of row-major, and no 16-sums are written.
 template <int BLK, bool TILED = false>
 __global__ __launch_bounds__(256) void quantize_q8_kernel(const float *__restrict__ x, int64_t M, int64_t K,
                                                           int8_t *__restrict__ q, float *__restrict__ d,
@@ -81,7 +81,7 @@ __global__ __launch_bounds__(256) void quantize_q8_kernel(const float *__restric
     s16 += __shfl_xor(s16, 1);
     s16 += __shfl_xor(s16, 2);
     if (!TILED && (l4 & 3) == 0) bs[off / 16] = (int16_t)s16;
-    if (TILED) {
+    if (TILED && sj) {  // q4_k: msum operands
         const int s32 = s16 + __shfl_xor(s16, 4);
         if ((l4 & 7) == 0) {
             const int j = l4 >> 3, sh = s32 >> 6, sl = s32 & 63;

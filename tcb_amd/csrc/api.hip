@@ -892,8 +892,8 @@ namespace {
 
 // Scratch layout of the act-quant operator: q [M][K] int8, d [M][K/blk] fp32, bs [M][K/16] int16, one NaN/Inf flag
 // byte per activation block, for q4_k the f16 msum operands [M][K/256][16], and an aligned copy of x when x is not
-// 16-byte aligned. When the q4_k prefill kernel takes the shape (tiles), q, d and the msum operands are in its
-// tiled layout over rows padded to a multiple of 128, and there are no 16-sums.
+// 16-byte aligned. When a prefill kernel (q4_k, q6_k) takes the shape (tiles), q, d and the q4_k msum operands are in
+// its tiled layout over rows padded to a multiple of 128, and there are no 16-sums.
 struct ActqLayout {
     size_t o_q = 0, o_d = 0, o_bs = 0, o_fl = 0, o_sj = 0, o_x = 0, total = 0;
     bool copy_x = false, tiles = false;
@@ -946,6 +946,7 @@ int actq_run(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, con
     if (l.tiles) {
         int st = launch_quantize_tiles(ctx, xa, M, K, q, d, sj, bad);
         if (st != TRHIP_OK) return st;
+        if (w->dtype == TRHIP_Q6K) return launch_prefill_q6k(ctx, w, row0, N, xa, c, M, accumulate != 0, q, d, bad);
         return launch_prefill_q4k(ctx, w, row0, N, xa, c, M, accumulate != 0, q, d, sj, bad, fast);
     }
     int st = launch_quantize_q8(ctx, xa, M, K, blk, q, d, bs, bad, sj);

@@ -1,6 +1,7 @@
-// prefill.hip -- act-quant prefill GEMM for q4_k weights on int8 MFMA, 128 activation rows x 32 weight rows per
-// wave, bit-identical to tensor/cpu_quant_q8.go:91-116 (dotQ4KQ8Go) like actq_mfma_q4k. Taken for grids large
-// enough to fill the device (at least 192 workgroups of 128 x 256).
+// prefill.hip -- act-quant prefill GEMM for q4_k (and, below, q6_k) weights on int8 MFMA, 128 activation rows x 32
+// weight rows per wave, bit-identical to tensor/cpu_quant_q8.go:91-116 (dotQ4KQ8Go) like actq_mfma_q4k, and to
+// :378-407 (dotQ6KQ8Go) for q6_k. Taken for grids large enough to fill the device (at least 192 workgroups of
+// 128 x 256).
 //
 // Arithmetic (same as actq_mfma_q4k): per block b and output (m, n), with sc_j = 8 s1 + s0,
 //   isum = sum_i (s0 q4)_i q8_i + 8 sum_i (s1 q4)_i q8_i      two v_mfma_i32_32x32x32_i8 accumulations, exact
@@ -50,12 +51,21 @@ static_assert(Pf::LDS <= 160 * 1024, "one workgroup per CU");
 // LDS read, so the next block's staging would never overlap the current block's work. The kernel waits for its copies
 // itself, once per block, before the barrier.
 
-// The per-block epilogue of one output: exact, in the reference's rounding order (seven VALU), or FAST, the same
-// integer sums with the two products and the accumulation fused (five VALU; within 1e-4 of the exact result).
-template <bool FAST>
+// Epilogue kinds: q4_k in the reference's rounding order, q4_k fast, q6_k (exact).
+enum { PF_Q4K = 0, PF_Q4K_FAST = 1, PF_Q6K = 2 };
+
+// The per-block epilogue of one output. q4_k (isum = p0 + 8 p1): exact, in the reference's rounding order (seven
+// VALU), or fast, the same integer sums with the two products and the accumulation fused (five VALU; within 1e-4 of
+// the exact result). q6_k (X = p0 + 128 p1, tensor/cpu_quant_q8.go:404-405): t = fl(d fl(X)), acc = fl(acc + fl(t d8))
+// (five VALU); cm and dm are not used.
+template <int EK>
 __device__ __forceinline__ float pf_epilogue(float acc, int p0, int p1, float cm, float dd, float dm, float d8) {
+    if (EK == PF_Q6K) {
+        const float tt = dd * (float)(p0 + 128 * p1);
+        return acc + tt * d8;
+    }
     const int isum = p0 + 8 * p1;
-    if (FAST) return fmaf(fmaf(-dm, cm, dd * (float)isum), d8, acc);
+    if (EK == PF_Q4K_FAST) return fmaf(fmaf(-dm, cm, dd * (float)isum), d8, acc);
     const float tt = (dd * (float)isum) - (dm * cm);
     return acc + tt * d8;
 }
@@ -78,7 +88,7 @@ __device__ __forceinline__ v8h small_f16x8(uint32_t lo, uint32_t hi, _Float16 c)
 // (p0, p1) with msum pcm, the pending block's d, dmin and the d8 of its rows (pd8, this lane's rows at + 8 (v / 4)
 // + (v % 4)). The pending sums are final only once the previous tile's last MFMAs have completed, so the first MFMA
 // pair runs alone and the sixteen outputs follow the next seven pairs (two each, four after the last).
-template <bool FAST>
+template <int EK>
 __device__ __forceinline__ void pf_tile(v16i &c0, v16i &c1, const v16i &p0, const v16i &p1, const v16f &pcm, float pdd,
                                         float pdm, float *pacc, const float *pd8, const v4i *ar, const v4i (&b0)[8],
                                         const v4i (&b1)[8]) {
@@ -91,7 +101,7 @@ __device__ __forceinline__ void pf_tile(v16i &c0, v16i &c1, const v16i &p0, cons
     a[1] = ar[64];
     float2 s8n = make_float2(0.0f, 0.0f);
     float4 s8q = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    constexpr int EV = FAST ? 5 : 7;
+    constexpr int EV = EK == PF_Q4K ? 7 : 5;
 #pragma unroll
     for (int kc = 0; kc < 8; kc++) {
         const float2 s8 = s8n;
@@ -110,7 +120,7 @@ __device__ __forceinline__ void pf_tile(v16i &c0, v16i &c1, const v16i &p0, cons
 #pragma unroll
             for (int r = 0; r < 2; r++) {
                 const int v = 2 * (kc - 1) + r;
-                pacc[v] = pf_epilogue<FAST>(pacc[v], p0[v], p1[v], pcm[v], pdd, pdm, s8v[r]);
+                pacc[v] = pf_epilogue<EK>(pacc[v], p0[v], p1[v], pcm[v], pdd, pdm, s8v[r]);
             }
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x002, EV, 0);
@@ -121,7 +131,7 @@ __device__ __forceinline__ void pf_tile(v16i &c0, v16i &c1, const v16i &p0, cons
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int v = 12 + r;
-                pacc[v] = pf_epilogue<FAST>(pacc[v], p0[v], p1[v], pcm[v], pdd, pdm, s8v[r]);
+                pacc[v] = pf_epilogue<EK>(pacc[v], p0[v], p1[v], pcm[v], pdd, pdm, s8v[r]);
             }
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x002, 2 * EV, 0);
@@ -139,7 +149,7 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
     const int8_t *__restrict__ qt, const float *__restrict__ dt, const uint16_t *__restrict__ st,
     const uint8_t *__restrict__ bad_blk, float *__restrict__ c) {
     using T = Pf;
-    constexpr int TM = T::TM, STAGE = T::STAGE, MT = PF_MT;
+    constexpr int TM = T::TM, STAGE = T::STAGE, MT = PF_MT, EK = FAST ? PF_Q4K_FAST : PF_Q4K;
     extern __shared__ __align__(16) uint8_t lds[];
     int *rowstate = reinterpret_cast<int *>(lds + T::DOFF + 3 * T::D);  // [TM] 0 ok, 1 NaN/Inf row, 2 outside M
     int *anybad = rowstate + TM;
@@ -263,21 +273,21 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
         // before its int8 MFMAs, into the msum set the pending epilogue does not read, so it has completed long
         // before that tile's own epilogue reads it
         pca = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[0], bmv, (v16f){0.0f}, 0, 0, 0);
-        pf_tile<FAST>(x0, x1, y0, y1, pcb, pdd, pdm, accf[MT - 1], d8p + 32 * (MT - 1), ar, b0, b1);
+        pf_tile<EK>(x0, x1, y0, y1, pcb, pdd, pdm, accf[MT - 1], d8p + 32 * (MT - 1), ar, b0, b1);
         pdd = dd;
         pdm = dm;
         pcb = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[64], bmv, (v16f){0.0f}, 0, 0, 0);
-        pf_tile<FAST>(y0, y1, x0, x1, pca, pdd, pdm, accf[0], d8b, ar + 512, b0, b1);
+        pf_tile<EK>(y0, y1, x0, x1, pca, pdd, pdm, accf[0], d8b, ar + 512, b0, b1);
         pca = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[128], bmv, (v16f){0.0f}, 0, 0, 0);
-        pf_tile<FAST>(x0, x1, y0, y1, pcb, pdd, pdm, accf[1], d8b + 32, ar + 1024, b0, b1);
+        pf_tile<EK>(x0, x1, y0, y1, pcb, pdd, pdm, accf[1], d8b + 32, ar + 1024, b0, b1);
         pcb = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[192], bmv, (v16f){0.0f}, 0, 0, 0);
-        pf_tile<FAST>(y0, y1, x0, x1, pca, pdd, pdm, accf[2], d8b + 64, ar + 1536, b0, b1);
+        pf_tile<EK>(y0, y1, x0, x1, pca, pdd, pdm, accf[2], d8b + 64, ar + 1536, b0, b1);
     }
     {  // the last block's last tile (set y, msum pcb)
         const float *d8l = reinterpret_cast<const float *>(lds + T::DOFF + ((nb + 2) % 3) * T::D) + lrow + 32 * (MT - 1);
 #pragma unroll
         for (int v = 0; v < 16; v++)
-            accf[MT - 1][v] = pf_epilogue<FAST>(accf[MT - 1][v], y0[v], y1[v], pcb[v], pdd, pdm, d8l[8 * (v >> 2) + (v & 3)]);
+            accf[MT - 1][v] = pf_epilogue<EK>(accf[MT - 1][v], y0[v], y1[v], pcb[v], pdd, pdm, d8l[8 * (v >> 2) + (v & 3)]);
     }
 
     const int64_t gn = n0 + nloc;
@@ -305,6 +315,213 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
     }
 }
 
+
+// q6_k (tensor/cpu_quant_q8.go:378-407). Per block, the wave's 32 weight rows' signed products
+// v = (q6 - 32) sc_j (the sub-block scale folded in; |v| <= 4096) are split as v = 128 h + l, h = v >> 7 in
+// [-32, 32] and l = v & 127 in [0, 127], both int8, so X = isum - 32 msum = sum v q8 = 128 sum h q8 + sum l q8:
+// two int8 MFMA accumulations over the whole block (l into the first set, h into the second) and the reference's
+// epilogue t = fl(d fl(X)), acc = fl(acc + fl(t d8)). Tiles, accumulator sets and the delayed epilogue are those of
+// prefill_q4k; there is no minimum term. The activation buffers are double-buffered as there; each wave's weight
+// rows have one buffer, refilled with the next block as soon as the wave has read the current one into registers.
+struct Pf6 {
+    static constexpr int TM = 32 * PF_MT;
+    static constexpr int A = PF_MT * 8192;                  // activation codes of one block (two buffers)
+    static constexpr int SC = 0, QL = 512, QH = QL + 4096;   // one wave's rows: 32 x 16 scales, 32 x 128 ql, 32 x 64 qh
+    static constexpr int WREG = QH + 2048;
+    static constexpr int W = 2 * A;                          // the waves' weight buffers
+    static constexpr int D = PF_MT * 128;                    // d8 of one block (slot b % 3, read one block later)
+    static constexpr int DOFF = W + PF_W * WREG;
+    static constexpr size_t LDS = DOFF + 3 * D + (TM + 1) * sizeof(int);
+};
+static_assert(Pf6::LDS <= 160 * 1024, "one workgroup per CU");
+
+typedef short pf_s2 __attribute__((ext_vector_type(2)));
+
+// Chunk kc's two B operands for lane (r, h): elements 32 kc + 16 h .. + 15 of the row, the four 4-element groups
+// e = 2 tt + hh (tt, hh in 0..1) from ql dword L[e] (nibble half k / 2) and qh dword H[e] (bit pair k = kc % 4), all
+// in sub-block 2 kc + h with signed scale sc. Per group: the codes c as bytes, spread to 16-bit pairs, v = c sc - 32 sc
+// by packed 16-bit multiply-adds, then the bytes of v >> 7 (h) and of v & 127 (l).
+__device__ __forceinline__ void q6_planes(const uint32_t (&L)[4], const uint32_t (&H)[4], int k, int sc, v4i &lo,
+                                          v4i &hi) {
+    const pf_s2 S = (pf_s2){(short)sc, (short)sc}, O = (pf_s2){(short)(-32 * sc), (short)(-32 * sc)};
+    uint32_t lb[4], hb[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const uint32_t lw = (k >> 1) ? (L[e] >> 4) : L[e];
+        const uint32_t hw = k == 0 ? (H[e] << 4) : k == 1 ? (H[e] << 2) : k == 2 ? H[e] : (H[e] >> 2);
+        const uint32_t C = (lw & 0x0F0F0F0Fu) | (hw & 0x30303030u);  // codes 0..63
+        const pf_s2 c01 = __builtin_bit_cast(pf_s2, __builtin_amdgcn_perm(0u, C, 0x0c010c00u));
+        const pf_s2 c23 = __builtin_bit_cast(pf_s2, __builtin_amdgcn_perm(0u, C, 0x0c030c02u));
+        const uint32_t v01 = __builtin_bit_cast(uint32_t, c01 * S + O), v23 = __builtin_bit_cast(uint32_t, c23 * S + O);
+        lb[e] = __builtin_amdgcn_perm(v23, v01, 0x06040200u) & 0x7F7F7F7Fu;  // low bytes, low 7 bits: v & 127
+        hb[e] = __builtin_amdgcn_perm(v23 >> 7, v01 >> 7, 0x06040200u);     // bits 7..14 of each v: v >> 7
+    }
+    lo = (v4i){(int)lb[0], (int)lb[1], (int)lb[2], (int)lb[3]};
+    hi = (v4i){(int)hb[0], (int)hb[1], (int)hb[2], (int)hb[3]};
+}
+
+template <bool ACC>
+__global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_q6k(
+    const Planes p, int64_t N, int64_t row0, int64_t M, int64_t K, const float *__restrict__ x,
+    const int8_t *__restrict__ qt, const float *__restrict__ dt, const uint8_t *__restrict__ bad_blk,
+    float *__restrict__ c) {
+    using T = Pf6;
+    constexpr int TM = T::TM, MT = PF_MT;
+    extern __shared__ __align__(16) uint8_t lds[];
+    int *rowstate = reinterpret_cast<int *>(lds + T::DOFF + 3 * T::D);  // [TM] 0 ok, 1 NaN/Inf row, 2 outside M
+    int *anybad = rowstate + TM;
+
+    const int nb = (int)p.nb;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int64_t tmi, tni;
+    tile_of(blockIdx.x, (M + TM - 1) / TM, (N + PF_TN - 1) / PF_TN, tmi, tni);
+    const int64_t n0 = tni * PF_TN, m0 = tmi * TM, mt0 = m0 >> 5;
+    tile_row_flags<TM, PF_THREADS>(bad_blk, m0, M, nb, rowstate, anybad);
+
+    const int nloc = 32 * w + (lane & 31);  // this lane's weight row (as the B operand: column lane % 32)
+    const int64_t mpad = (M + TM - 1) / TM * TM;
+    const dma_rsrc rq = dma_desc(qt, (uint32_t)(mpad * nb * 256));
+    const dma_rsrc rd = dma_desc(dt, (uint32_t)(mpad * nb * 4));
+    const dma_rsrc rwl = dma_desc(p.qs, (uint32_t)((row0 + N) * nb * 128));
+    const dma_rsrc rwh = dma_desc(p.aux, (uint32_t)((row0 + N) * nb * 64));
+    const dma_rsrc rws = dma_desc(p.sc, (uint32_t)((row0 + N) * nb * 16));
+    // this wave's rows (rows past row0 + N read zeros from the buffers' bounds; their outputs are not stored)
+    const int64_t wr0 = row0 + n0 + 32 * w;
+    const uint32_t wl0 = (uint32_t)(wr0 * nb * 128), wh0 = (uint32_t)(wr0 * nb * 64), ws0 = (uint32_t)(wr0 * nb * 16);
+    uint8_t *wb = lds + T::W + w * T::WREG;
+    // d of this lane's row, one block ahead in a register (plain loads)
+    const int64_t drow = wr0 + (lane & 31) < row0 + N ? wr0 + (lane & 31) : row0 + N - 1;
+    const uint16_t *dp = p.d + drow * nb;
+
+    // activation codes (tile t chunk w per wave) and the d8 pieces (two tiles each, waves 0 .. MT / 2 - 1) of block
+    // b into buffer buf, as in prefill_q4k
+    auto stage_act = [&](int b, int buf) {
+        const uint32_t ln = opaque((uint32_t)lane);
+        const uint32_t v16 = 16 * ln, vd = (ln >> 5) * (uint32_t)nb * 128 + 4 * (ln & 31);
+        uint8_t *sb = lds + buf * T::A;
+        uint8_t *db = lds + T::DOFF + (b % 3) * T::D;
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+            dma16(rq, lds_addr(sb + 1024 * (8 * t + w)), v16, (uint32_t)((((mt0 + t) * nb + b) * 8 + w) * 1024));
+        if (w < MT / 2) dma4(rd, lds_addr(db + 256 * w), vd, (uint32_t)(((mt0 + 2 * w) * nb + b) * 128));
+    };
+    // this wave's rows of block b: scales by dwords (16 rows per instruction); ql as prefill_q4k's codes (eight rows
+    // per instruction, slot s of row r holding piece s ^ ((r / 2) % 8)); qh 16 rows per instruction, slot s of row r
+    // holding piece s ^ ((r / 4) % 4), so that the 16 rows a b128 read pass covers hit 16 different bank groups
+    auto stage_w = [&](int b) {
+        const uint32_t ln = opaque((uint32_t)lane);
+        const uint32_t vs = (ln >> 2) * (uint32_t)nb * 16 + 4 * (ln & 3);
+        const uint32_t jr = ln >> 3, jc = ln & 7;
+        const uint32_t vl0 = jr * (uint32_t)nb * 128 + 16 * (jc ^ (jr >> 1)), vl1 = vl0 ^ 64;
+        const uint32_t hr = ln >> 2, hc = ln & 3;
+        const uint32_t vh = hr * (uint32_t)nb * 64 + 16 * (hc ^ ((hr >> 2) & 3));
+#pragma unroll
+        for (int q = 0; q < 2; q++) dma4(rws, lds_addr(wb + T::SC + 256 * q), vs, ws0 + (uint32_t)(16 * b + 256 * q * nb));
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            dma16(rwl, lds_addr(wb + T::QL + 1024 * q), (q & 1) ? vl1 : vl0, wl0 + (uint32_t)(128 * b + 1024 * q * nb));
+#pragma unroll
+        for (int q = 0; q < 2; q++)
+            dma16(rwh, lds_addr(wb + T::QH + 1024 * q), vh, wh0 + (uint32_t)(64 * b + 1024 * q * nb));
+    };
+
+    stage_act(0, 0);
+    stage_w(0);
+    uint16_t draw = dp[0];
+
+    float accf[MT][16];
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) accf[t][v] = 0.0f;
+    // pending epilogue state as in prefill_q4k (nothing pending before the first block: zero sums, zero d8)
+    v16i x0 = (v16i){0}, x1 = (v16i){0}, y0 = (v16i){0}, y1 = (v16i){0};
+    const v16f nocm = (v16f){0.0f};
+    float pdd = 0.0f;
+    if (tid < T::D / 4) reinterpret_cast<float *>(lds + T::DOFF + 2 * T::D)[tid] = 0.0f;
+    const int lrow = 4 * (lane >> 5);
+
+    for (int b = 0; b < nb; b++) {
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        // d of block b (loaded during the previous block) is used before the next copies are issued, so the wait the
+        // compiler places for that load cannot fall after them
+        const float dd = f16_to_f32(draw);
+        asm volatile("" ::"v"(dd));
+        if (b + 1 < nb) stage_act(b + 1, (b + 1) & 1);
+        const uint8_t *sb = lds + (b & 1) * T::A;
+
+        // this lane's bytes of the block: ql pieces 4 h + g, qh pieces 2 h + tt, the row's 16 scales
+        const int ln = (int)opaque((uint32_t)lane), r = ln & 31, h = ln >> 5;
+        uint4 wq[4], qq[2];
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+            wq[g] = *reinterpret_cast<const uint4 *>(wb + T::QL + 128 * r + 16 * ((4 * h + g) ^ ((r >> 1) & 7)));
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++)
+            qq[tt] = *reinterpret_cast<const uint4 *>(wb + T::QH + 64 * r + 16 * ((2 * h + tt) ^ ((r >> 2) & 3)));
+        const uint4 scw = *reinterpret_cast<const uint4 *>(wb + T::SC + 16 * r);
+        // every read of the buffer has landed: refill it with the next block, and load its d
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (b + 1 < nb) stage_w(b + 1);
+        draw = dp[b + 1 < nb ? b + 1 : b];
+        v4i b0[8], b1[8];
+#pragma unroll
+        for (int kc = 0; kc < 8; kc++) {
+            const int n2 = kc >> 2, k = kc & 3, kk = k & 1;
+            uint32_t L[4], H[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint4 lq = wq[n2 + 2 * (e >> 1)], hq = qq[e >> 1];
+                const int ld = 2 * kk + (e & 1), hd = 2 * n2 + (e & 1);
+                L[e] = ld == 0 ? lq.x : ld == 1 ? lq.y : ld == 2 ? lq.z : lq.w;
+                H[e] = hd == 0 ? hq.x : hd == 1 ? hq.y : hd == 2 ? hq.z : hq.w;
+            }
+            const uint32_t sw = (kc >> 1) == 0 ? scw.x : (kc >> 1) == 1 ? scw.y : (kc >> 1) == 2 ? scw.z : scw.w;
+            const int sc = __builtin_amdgcn_sbfe((int)sw, 16 * (kc & 1) + 8 * h, 8);  // sub-block 2 kc + h
+            q6_planes(L, H, k, sc, b0[kc], b1[kc]);
+        }
+
+        const v4i *ar = reinterpret_cast<const v4i *>(sb) + ln;  // tile t, chunk kc: + 512 t + 64 kc
+        const float *d8b = reinterpret_cast<const float *>(lds + T::DOFF + (b % 3) * T::D) + 4 * h;
+        const float *d8p = reinterpret_cast<const float *>(lds + T::DOFF + ((b + 2) % 3) * T::D) + 4 * h;
+        pf_tile<PF_Q6K>(x0, x1, y0, y1, nocm, pdd, 0.0f, accf[MT - 1], d8p + 32 * (MT - 1), ar, b0, b1);
+        pdd = dd;
+        pf_tile<PF_Q6K>(y0, y1, x0, x1, nocm, pdd, 0.0f, accf[0], d8b, ar + 512, b0, b1);
+        pf_tile<PF_Q6K>(x0, x1, y0, y1, nocm, pdd, 0.0f, accf[1], d8b + 32, ar + 1024, b0, b1);
+        pf_tile<PF_Q6K>(y0, y1, x0, x1, nocm, pdd, 0.0f, accf[2], d8b + 64, ar + 1536, b0, b1);
+    }
+    {  // the last block's last tile (set y)
+        const float *d8l = reinterpret_cast<const float *>(lds + T::DOFF + ((nb + 2) % 3) * T::D) + lrow + 32 * (MT - 1);
+#pragma unroll
+        for (int v = 0; v < 16; v++)
+            accf[MT - 1][v] = pf_epilogue<PF_Q6K>(accf[MT - 1][v], y0[v], y1[v], 0.0f, pdd, 0.0f, d8l[8 * (v >> 2) + (v & 3)]);
+    }
+
+    const int64_t gn = n0 + nloc;
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int mloc = 32 * t + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+            if (gn < N && rowstate[mloc] == 0) {
+                float *o = c + (m0 + mloc) * N + gn;
+                *o = ACC ? *o + accf[t][v] : accf[t][v];
+            }
+        }
+    }
+    // rows holding NaN/Inf take the exact fp32 path (quantGemv) on their own; rare
+    if (!*anybad) return;
+    for (int i = tid; i < TM * PF_TN; i += PF_THREADS) {
+        const int ml = i / PF_TN, nl = i % PF_TN;
+        const int64_t gn2 = n0 + nl;
+        if (rowstate[ml] != 1 || gn2 >= N) continue;
+        const int64_t gm = m0 + ml;
+        const float v = exact_dot_row<kQ6K>(p, row0 + gn2, x + gm * K, K);
+        float *o = c + gm * N + gn2;
+        *o = ACC ? *o + v : v;
+    }
+}
 }  // namespace
 
 // Taken when the grid of 128 x 256 tiles has at least 192 workgroups (one per CU fits), else the 64-row kernel of
@@ -318,7 +535,7 @@ bool prefill_fits32(int64_t M, int64_t N, int64_t row0, int64_t K) {
 }  // namespace
 
 bool prefill_tiles_apply(int dtype, int64_t M, int64_t N, int64_t row0, int64_t K) {
-    if (dtype != kQ4K || !prefill_fits32(M, N, row0, K)) return false;
+    if ((dtype != kQ4K && dtype != kQ6K) || !prefill_fits32(M, N, row0, K)) return false;
     const int64_t wgs = ((M + Pf::TM - 1) / Pf::TM) * ((N + PF_TN - 1) / PF_TN);
     return M >= 256 && wgs >= 192;
 }
@@ -340,6 +557,23 @@ int launch_prefill_q4k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int6
     };
     if (fast) return acc ? go(&prefill_q4k<true, true>) : go(&prefill_q4k<false, true>);
     return acc ? go(&prefill_q4k<true, false>) : go(&prefill_q4k<false, false>);
+}
+
+int launch_prefill_q6k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
+                       int64_t M, bool acc, const int8_t *qt, const float *dt, const uint8_t *bad) {
+    using T = Pf6;
+    static_assert(T::TM == kPrefillRowPad, "the tiled layout pads rows to one workgroup row tile");
+    const int64_t wgs = ((M + T::TM - 1) / T::TM) * ((N + PF_TN - 1) / PF_TN);
+    if (wgs >= ((int64_t)1 << 31)) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "prefill: grid too large");
+    if (!prefill_fits32(M, N, row0, w->K)) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "prefill: buffers above 4 GB");
+    auto go = [&](auto kern) {
+        int st0 = allow_dyn_lds(ctx, reinterpret_cast<const void *>(kern), T::LDS, "prefill: LDS size");
+        if (st0 != TRHIP_OK) return st0;
+        hipLaunchKernelGGL(kern, dim3((unsigned)wgs), dim3(PF_THREADS), T::LDS, ctx->stream, w->planes(), N, row0, M,
+                           w->K, x, qt, dt, bad, c);
+        return launch_check(ctx, "prefill_q6k");
+    };
+    return acc ? go(&prefill_q6k<true>) : go(&prefill_q6k<false>);
 }
 
 }  // namespace trhip

@@ -473,27 +473,58 @@ def test_actq_prefill_other_dtypes_bits(backend, dt, N, K, M):
     w.release()
 
 
+@pytest.mark.parametrize("dt", [Q4K, Q6K])
 @pytest.mark.parametrize("M,N,K,row0,acc,x_off", [(300, 16421, 512, 5, True, 0), (257, 49153, 256, 0, False, 4),
-                                                  (384, 12800, 1024, 0, True, 0)])
-def test_prefill_tiles_bits(backend, M, N, K, row0, acc, x_off):
-    """The 128-row-per-wave prefill kernel (taken for grids of at least 384 128x128 tiles): rows padded past M,
-    ragged N, a row slice of the store, both accumulate modes, an unaligned x, x1000 / zero / +-1 rows and a NaN row
-    (its outputs from the fp32 path): bit-identical to the oracle."""
+                                                  (384, 12800, 1024, 0, True, 0), (260, 16640, 768, 9, False, 0)])
+def test_prefill_tiles_bits(backend, dt, M, N, K, row0, acc, x_off):
+    """The 128-row-per-wave prefill kernels, q4_k and q6_k (taken for grids of at least 192 128x256 tiles; 384 x
+    12800 is below that and takes the other kernels): rows padded past M, ragged N, a row slice of the store, both
+    accumulate modes, an unaligned x, x1000 / zero / +-1 rows and a NaN row (its outputs from the fp32 path), on TR's
+    random-scale blocks (q6_k: signed sub-block scales of every magnitude): bit-identical to the oracle."""
     rng = _rng(M + N + K)
-    raw = _weights(Q4K, row0 + N, K, M * 3 + K)
+    raw = _weights(dt, row0 + N, K, M * 3 + K)
     X = _x(rng, M * K).reshape(M, K)
     X[1] *= 1000
     X[2, :256] = 0
     X[3] = 1 - 2 * (np.arange(K) % 2)
     X[M - 2, 11] = np.nan
-    w = backend.FromQuantized(Q4K, raw, row0 + N, K)
+    w = backend.FromQuantized(dt, raw, row0 + N, K)
     c0 = _x(rng, M * N) if acc else np.zeros(M * N, np.float32)
     xb = backend.ctx.alloc(M * K * 4 + 16)
     xb.upload(X, byte_offset=x_off)
     cb = backend.ctx.to_device(c0)
     backend.GemmActQuant(M, N, K, (xb, x_off), w, cb, row0=row0, accumulate=acc)
     rows = np.ascontiguousarray(raw.reshape(row0 + N, -1)[row0:])
-    same_bits(cb.download(np.float32, M * N), O.quant_gemm_act(Q4K, M, N, K, X, rows, c0))
+    same_bits(cb.download(np.float32, M * N), O.quant_gemm_act(dt, M, N, K, X, rows, c0))
+    for b in (xb, cb):
+        b.free()
+    w.release()
+
+
+def test_prefill_q6k_extreme_bits(backend):
+    """q6_k prefill at the ends of the plane split: codes 0 and 63 under sub-block scales -128, -1, 0, 1 and 127 (the
+    products (q - 32) sc reach 4096, -4064 and 3937), against activations at the code limits +-127 (constant rows,
+    alternating rows) and ordinary rows: bit-identical to the oracle."""
+    M, N, K = 256, 24576, 512
+    rng = _rng(7)
+    nb = K // 256
+    blk = np.zeros((N, nb, 210), np.uint8)
+    code = rng.integers(0, 2, size=(N, nb)) * 63  # all codes 0 or all 63 per block
+    blk[:, :, 0:128] = np.where(code[..., None] == 63, 0xFF, 0x00)
+    blk[:, :, 128:192] = np.where(code[..., None] == 63, 0xFF, 0x00)
+    scales = np.array([-128, -1, 0, 1, 127], np.int8).view(np.uint8)
+    blk[:, :, 192:208] = scales[rng.integers(0, 5, size=(N, nb, 16))]
+    blk[:, :, 208:210] = np.array([0x00, 0x3C], np.uint8)  # d = 1.0
+    raw = blk.reshape(-1)
+    X = _x(rng, M * K).reshape(M, K)
+    X[0] = 3.0
+    X[1] = -3.0
+    X[2] = np.where(np.arange(K) % 2 == 0, 5.0, -5.0)
+    X[3, ::256] = 100.0
+    w = backend.FromQuantized(Q6K, raw, N, K)
+    xb, cb = backend.ctx.to_device(X), backend.ctx.alloc(M * N * 4)
+    backend.GemmActQuant(M, N, K, xb, w, cb, accumulate=False)
+    same_bits(cb.download(np.float32, M * N), O.quant_gemm_act(Q6K, M, N, K, X, raw))
     for b in (xb, cb):
         b.free()
     w.release()
