@@ -55,8 +55,10 @@ __device__ __forceinline__ void q4a_dma4(dma_rsrc r, uint32_t voffset, uint32_t 
 __device__ __forceinline__ int q4a_act_slot(int row, int c) { return 16 * row + (c ^ (row & 15)); }
 __device__ __forceinline__ int q4a_w_slot(int row, int bb) { return 8 * row + (bb ^ (row & 7)); }
 
+// (two waves per SIMD, which the LDS allows anyway: with the register budget of that occupancy the products stay in
+// VGPRs, and the epilogue reads them without a copy out of the accumulator registers)
 template <bool ACC>
-__global__ __launch_bounds__(Q4A_THREADS) void actq4_mfma(const Planes p, int64_t N, int64_t row0, int64_t M,
+__global__ __launch_bounds__(Q4A_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void actq4_mfma(const Planes p, int64_t N, int64_t row0, int64_t M,
                                                           int64_t K, const float *__restrict__ x,
                                                           const int8_t *__restrict__ q, const float *__restrict__ d8g,
                                                           const uint8_t *__restrict__ bad_blk, float *__restrict__ c) {
