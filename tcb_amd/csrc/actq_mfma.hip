@@ -792,6 +792,11 @@ constexpr int FH_PLANE = 8 * 1024;                   // one f16 plane of a 16-ro
 constexpr int FH_STAGE = 2 * FH_PLANE + F16_TM * 4;  // hi, lo, exponents
 constexpr size_t FH_LDS = 2 * FH_STAGE + (F16_TM + 1) * sizeof(int);
 
+// Operand lane l of step s sits in slot fh_swz(l, s) of the step's 64: its row bits (l % 16) XOR 4 (l / 16) + s % 4.
+// A wave's stage writes (two rows, all 32 pieces of each) then spread over every bank group, and the MFMA's reads of
+// a step stay a permutation within each 16-lane group.
+__device__ __forceinline__ int fh_swz(int l, int s) { return l ^ ((4 * (l >> 4) + (s & 3)) & 15); }
+
 // One wave per (row m, chunk b): exponent, the two f16 planes and the NaN/Inf flag.
 __global__ __launch_bounds__(256) void halves_kernel(const float *__restrict__ x, int64_t M, int64_t K,
                                                      uint16_t *__restrict__ hi, uint16_t *__restrict__ lo,
@@ -887,14 +892,15 @@ __global__ __launch_bounds__(FM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
     tile_row_flags<F16_TM, FM_THREADS>(bad, m0, M, nc, rowbad, anybad);
 
     // staging: 16-byte pieces P = tid and tid + 256 of each plane: row P / 32, piece j = P % 32 (halves 8j .. +7)
-    // = step j / 4, k-slice j % 4, i.e. slot 64 (j / 4) + 16 (j % 4) + row; threads < 16 one exponent
+    // = step j / 4, k-slice j % 4, i.e. lane 16 (j % 4) + row of step j / 4, at slot fh_swz(lane, step) of the step;
+    // threads < 16 one exponent
     const uint16_t *hsrc[2];
     int hslot[2];
 #pragma unroll
     for (int i = 0; i < 2; i++) {
         const int P = tid + 256 * i, r = P >> 5, j = P & 31;
         hsrc[i] = xh + (m0 + r < M ? m0 + r : M - 1) * K + 8 * j;
-        hslot[i] = 64 * (j >> 2) + 16 * (j & 3) + r;
+        hslot[i] = 64 * (j >> 2) + fh_swz(16 * (j & 3) + r, j >> 2);
     }
     const int64_t lo_off = xl - xh;  // the lo plane sits at the same offsets from xl
     const int64_t egm = m0 + (tid & 15) < M ? m0 + (tid & 15) : M - 1;
@@ -955,7 +961,7 @@ __global__ __launch_bounds__(FM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
         v4f acc[2] = {zero, zero};
 #pragma unroll
         for (int s = 0; s < 8; s++) {
-            const v8h ah = ph[64 * s + lane], al = pq[64 * s + lane];
+            const v8h ah = ph[64 * s + fh_swz(lane, s)], al = pq[64 * s + fh_swz(lane, s)];
 #pragma unroll
             for (int t = 0; t < 2; t++) {
                 const v8h q = q6_codes(cw[t], s);

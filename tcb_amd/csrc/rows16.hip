@@ -204,8 +204,10 @@ struct R16Stage {  // one block in LDS: the activation record, the R rows' heade
 
 // DT: q4_k, or q4_0 (its 256-element chunk holds eight blocks: the 16-byte header of a row's chunk is the blocks'
 // eight fp16 scales, its 128 qs bytes their codes, so the staging is the same)
+// (two waves per SIMD, which the LDS allows anyway: with the register budget of that occupancy the products stay in
+// VGPRs rather than being copied out of the accumulator registers)
 template <int DT, int TPW, bool ACC, bool SWI>
-__global__ __launch_bounds__(R16_THREADS) void rows16_gemm(const Planes p, int64_t nrows, int64_t N, int64_t row0,
+__global__ __launch_bounds__(R16_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void rows16_gemm(const Planes p, int64_t nrows, int64_t N, int64_t row0,
                                                            int64_t M, int64_t K, const float *__restrict__ x,
                                                            const uint8_t *__restrict__ rec, int64_t RT, int S, int bps,
                                                            float *__restrict__ c, float *__restrict__ part,
