@@ -423,6 +423,28 @@ def mfma_rate(tb, valu_per_mfma, waves_per_simd, iters=40000):
     return 4.0 * waves_per_simd * cus * iters * 4 * 65536 / (ms * 1e-3) / 1e12
 
 
+def prefill_loop_us(tb, kind, M, N, K, reps=20):
+    """Microseconds per launch of trhip_prefill_probe (the prefill kernel's inner loop alone on its real grid: kind 0
+    q4_k exact, 1 q4_k fast, 2 q6_k), median of reps event-timed launches after two warm-up launches."""
+    from tcb_amd import _lib
+    L = _lib.lib()
+    ctx = tb.ctx
+    for _ in range(2):
+        if L.trhip_prefill_probe(ctx.h, kind, M, N, K):
+            raise RuntimeError("prefill probe failed")
+    ctx.sync()
+    ts = []
+    for _ in range(reps):
+        e0, e1 = ctx.event(), ctx.event()
+        ctx.record(e0)
+        L.trhip_prefill_probe(ctx.h, kind, M, N, K)
+        ctx.record(e1)
+        ctx.sync()
+        ts.append(ctx.elapsed_ms(e0, e1) * 1e3)
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
 def upload_rates(tb, raw):
     """Store creation (upload + repack) of the headline weights: GB/s of GGUF bytes from pageable host memory and
     from a trhip_host_alloc (pinned) block, median of 5."""
@@ -568,6 +590,8 @@ def main():
         tops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
         ceiling = mfma_rate(tb, 0, 2)
         ceiling7 = mfma_rate(tb, 6, 2)
+        loop_us = prefill_loop_us(tb, 1 if mode == MODE_FAST else 0, M, N, K)
+        loop_us_q6 = prefill_loop_us(tb, 2, M, N, K)
         prefill = {"workload": "act-quant GEMM q4_k %dx%d, M=%d (quantize + int block sums + fp32 epilogue)" % (N, K, M),
                    "mode": a.mode, "us": round(ms * 1e3, 2), "int8_tops": round(tops, 2),
                    "frac_of_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
@@ -576,6 +600,11 @@ def main():
                    "measured_int8_mfma_tops": round(ceiling, 1),
                    "measured_int8_mfma_tops_6valu": round(ceiling7, 1),
                    "frac_of_measured_int8": round(tops / ceiling, 4),
+                   "inner_loop": {"us": round(loop_us, 2),
+                                  "frac_of_int8_peak": round(2.0 * M * N * K / (loop_us * 1e-6) / 1e12 / INT8_PEAK_TOPS, 4),
+                                  "q6_k_us": round(loop_us_q6, 2),
+                                  "what": "trhip_prefill_probe: the kernel's per-block loop on the same grid, staging, "
+                                          "barriers and stores taken out (events, median of 20)"},
                    "traffic_bytes": PREFILL_TRAFFIC if M == 512 else None,
                    "traffic_source": "rocprofv3 FETCH_SIZE + WRITE_SIZE over --profile-kernel prefill, kept in "
                                      "profiles/prefill_q4_k_14336x4096_M512.txt (not measured in this run)"}

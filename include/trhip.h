@@ -217,6 +217,12 @@ int trhip_read_probe(trhip_ctx *ctx, const void *p, int64_t bytes);
  * int8 matrix-core rate and how much VALU work hides under it, the ceiling of the prefill kernel. */
 int trhip_mfma_probe(trhip_ctx *ctx, int valu_per_mfma, int waves_per_simd, int64_t iters);
 
+/* Diagnostic with no counterpart in the reference: the act-quant prefill kernel's inner loop alone (kind 0: q4_k
+ * exact, 1: q4_k fast, 2: q6_k), on the grid trhip_gemm_q_actq launches for M x N x K, with its LDS staging, its
+ * per-block barrier and its stores taken out (weights and activations are not read). Timed with events it gives the
+ * ceiling of the loop the prefill kernel runs per block. Refused during graph capture. */
+int trhip_prefill_probe(trhip_ctx *ctx, int kind, int64_t M, int64_t N, int64_t K);
+
 /* Test and tuning hook with no counterpart in the reference: force a launch shape on this context
  * instead of the built-in choice (all four values 0 restores it). Shapes that are not built are
  * refused here, never at a later GEMV. TRHIP_KNOB_KL: K-across-lanes fast GEMV (a, b, c, d) =

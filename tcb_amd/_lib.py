@@ -53,6 +53,7 @@ SIGNATURES = [
     ("trhip_open_q", INT, [P, P, I64, I64, P]),
     ("trhip_read_probe", INT, [P, P, I64]),
     ("trhip_mfma_probe", INT, [P, INT, INT, I64]),
+    ("trhip_prefill_probe", INT, [P, INT, I64, I64, I64]),
     ("trhip_embedding_q", INT, [P, P, P, I64, P]),
     ("trhip_quantize_q8", INT, [P, P, I64, I64, INT, P, P, P]),
     ("trhip_swiglu", INT, [P, P, I64, I64, P]),

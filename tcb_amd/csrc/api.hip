@@ -1048,6 +1048,12 @@ int trhip_mfma_probe(trhip_ctx *ctx, int valu_per_mfma, int waves_per_simd, int6
     return launch_mfma_probe(ctx, valu_per_mfma, waves_per_simd, iters);
 }
 
+int trhip_prefill_probe(trhip_ctx *ctx, int kind, int64_t M, int64_t N, int64_t K) {
+    if (!ctx) return TRHIP_ERR_INVALID;
+    DevGuard g(ctx);
+    return launch_prefill_probe(ctx, kind, M, N, K);
+}
+
 int trhip_embedding_q(trhip_ctx *ctx, const trhip_wstore *w, const int64_t *idx, int64_t nidx, float *out) {
     if (!ctx || !w || nidx < 0) return TRHIP_ERR_INVALID;
     if (nidx == 0) return TRHIP_OK;

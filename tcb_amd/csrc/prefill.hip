@@ -143,7 +143,15 @@ __device__ __forceinline__ void pf_tile(v16i &c0, v16i &c1, const v16i &p0, cons
     }
 }
 
-template <bool ACC, bool FAST>
+// Zero the first `bytes` of the workgroup's LDS (16-byte stores; bytes a multiple of 16), then a barrier.
+__device__ __forceinline__ void pf_probe_fill(uint8_t *lds, int bytes, int tid) {
+    for (int o = 16 * tid; o < bytes; o += 16 * PF_THREADS) *reinterpret_cast<uint4 *>(lds + o) = make_uint4(0, 0, 0, 0);
+    __syncthreads();
+}
+
+// PROBE: the same kernel without its staging (no copies, no per-block wait and barrier; LDS zero-filled once) and
+// with c null (nothing stored), which times the inner loop alone on the real grid (trhip_prefill_probe).
+template <bool ACC, bool FAST, bool PROBE = false>
 __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_q4k(
     const Planes p, int64_t N, int64_t row0, int64_t M, int64_t K, const float *__restrict__ x,
     const int8_t *__restrict__ qt, const float *__restrict__ dt, const uint16_t *__restrict__ st,
@@ -214,7 +222,10 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
             dma16(rwq, lds_addr(wb + 512 + 1024 * q), (q & 1) ? vq1 : vq0, wq0 + (uint32_t)(128 * b + 1024 * q * nb));
     };
 
-    stage(0, 0);
+    if (PROBE)
+        pf_probe_fill(lds, T::DOFF + 3 * T::D, tid);
+    else
+        stage(0, 0);
 
     float accf[MT][16];
 #pragma unroll
@@ -233,8 +244,10 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
     for (int b = 0; b < nb; b++) {
         // this wave's loads of block b have landed; after the barrier everyone's have, and nobody reads the other
         // buffer (block b - 1) any more
-        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        if (b + 1 < nb) stage(b + 1, (b + 1) & 1);
+        if (!PROBE) {
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            if (b + 1 < nb) stage(b + 1, (b + 1) & 1);
+        }
         const uint8_t *sb = lds + (b & 1) * STAGE;
 
         // weight block b from LDS: scales and both planes of all eight sub-blocks
@@ -296,7 +309,7 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
 #pragma unroll
         for (int v = 0; v < 16; v++) {
             const int mloc = 32 * t + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-            if (gn < N && rowstate[mloc] == 0) {
+            if ((!PROBE || c) && gn < N && rowstate[mloc] == 0) {
                 float *o = c + (m0 + mloc) * N + gn;
                 *o = ACC ? *o + accf[t][v] : accf[t][v];
             }
@@ -360,7 +373,7 @@ __device__ __forceinline__ void q6_planes(const uint32_t (&L)[4], const uint32_t
     hi = (v4i){(int)hb[0], (int)hb[1], (int)hb[2], (int)hb[3]};
 }
 
-template <bool ACC>
+template <bool ACC, bool PROBE = false>  // PROBE: as for prefill_q4k
 __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_q6k(
     const Planes p, int64_t N, int64_t row0, int64_t M, int64_t K, const float *__restrict__ x,
     const int8_t *__restrict__ qt, const float *__restrict__ dt, const uint8_t *__restrict__ bad_blk,
@@ -426,9 +439,14 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
             dma16(rwh, lds_addr(wb + T::QH + 1024 * q), vh, wh0 + (uint32_t)(64 * b + 1024 * q * nb));
     };
 
-    stage_act(0, 0);
-    stage_w(0);
-    uint16_t draw = dp[0];
+    uint16_t draw = 0x3C00;  // (the probe's d: 1.0)
+    if (PROBE) {
+        pf_probe_fill(lds, T::DOFF + 3 * T::D, tid);
+    } else {
+        stage_act(0, 0);
+        stage_w(0);
+        draw = dp[0];
+    }
 
     float accf[MT][16];
 #pragma unroll
@@ -443,12 +461,12 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
     const int lrow = 4 * (lane >> 5);
 
     for (int b = 0; b < nb; b++) {
-        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (!PROBE) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
         // d of block b (loaded during the previous block) is used before the next copies are issued, so the wait the
         // compiler places for that load cannot fall after them
         const float dd = f16_to_f32(draw);
         asm volatile("" ::"v"(dd));
-        if (b + 1 < nb) stage_act(b + 1, (b + 1) & 1);
+        if (!PROBE && b + 1 < nb) stage_act(b + 1, (b + 1) & 1);
         const uint8_t *sb = lds + (b & 1) * T::A;
 
         // this lane's bytes of the block: ql pieces 4 h + g, qh pieces 2 h + tt, the row's 16 scales
@@ -463,8 +481,10 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
         const uint4 scw = *reinterpret_cast<const uint4 *>(wb + T::SC + 16 * r);
         // every read of the buffer has landed: refill it with the next block, and load its d
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        if (b + 1 < nb) stage_w(b + 1);
-        draw = dp[b + 1 < nb ? b + 1 : b];
+        if (!PROBE) {
+            if (b + 1 < nb) stage_w(b + 1);
+            draw = dp[b + 1 < nb ? b + 1 : b];
+        }
         v4i b0[8], b1[8];
 #pragma unroll
         for (int kc = 0; kc < 8; kc++) {
@@ -504,7 +524,7 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2
 #pragma unroll
         for (int v = 0; v < 16; v++) {
             const int mloc = 32 * t + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-            if (gn < N && rowstate[mloc] == 0) {
+            if ((!PROBE || c) && gn < N && rowstate[mloc] == 0) {
                 float *o = c + (m0 + mloc) * N + gn;
                 *o = ACC ? *o + accf[t][v] : accf[t][v];
             }
@@ -574,6 +594,42 @@ int launch_prefill_q6k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int6
         return launch_check(ctx, "prefill_q6k");
     };
     return acc ? go(&prefill_q6k<true>) : go(&prefill_q6k<false>);
+}
+
+int launch_prefill_probe(trhip_ctx *ctx, int kind, int64_t M, int64_t N, int64_t K) {
+    if (kind < 0 || kind > 2 || M <= 0 || N <= 0 || K <= 0 || K % 256 != 0)
+        return fail(ctx, TRHIP_ERR_INVALID, "prefill_probe: kind 0..2, M, N > 0 and K a positive multiple of 256");
+    if (capturing(ctx)) return fail(ctx, TRHIP_ERR_INVALID, "prefill_probe: not capturable");
+    const int64_t nb = K / 256, TM = Pf::TM;
+    const int64_t wgs = ((M + TM - 1) / TM) * ((N + PF_TN - 1) / PF_TN);
+    if (wgs >= ((int64_t)1 << 31)) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "prefill_probe: grid too large");
+    // the row flags the kernels read (every activation row finite); weights and activations are not read
+    int st = TRHIP_OK;
+    uint8_t *flags = static_cast<uint8_t *>(workspace(ctx, (size_t)(M * nb), &st));
+    if (!flags) return st;
+    hipError_t e = hipMemsetAsync(flags, 0, (size_t)(M * nb), ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "prefill_probe: flags");
+    Planes pl{};
+    pl.nb = nb;
+    auto go = [&](auto kern, size_t lds) {
+        int st0 = allow_dyn_lds(ctx, reinterpret_cast<const void *>(kern), lds, "prefill_probe: LDS size");
+        if (st0 != TRHIP_OK) return st0;
+        return 0;
+    };
+    if (kind == 2) {
+        if ((st = go(&prefill_q6k<false, true>, Pf6::LDS)) != TRHIP_OK) return st;
+        hipLaunchKernelGGL((prefill_q6k<false, true>), dim3((unsigned)wgs), dim3(PF_THREADS), Pf6::LDS, ctx->stream, pl,
+                           N, (int64_t)0, M, K, nullptr, nullptr, nullptr, flags, nullptr);
+    } else if (kind == 1) {
+        if ((st = go(&prefill_q4k<false, true, true>, Pf::LDS)) != TRHIP_OK) return st;
+        hipLaunchKernelGGL((prefill_q4k<false, true, true>), dim3((unsigned)wgs), dim3(PF_THREADS), Pf::LDS, ctx->stream,
+                           pl, N, (int64_t)0, M, K, nullptr, nullptr, nullptr, nullptr, flags, nullptr);
+    } else {
+        if ((st = go(&prefill_q4k<false, false, true>, Pf::LDS)) != TRHIP_OK) return st;
+        hipLaunchKernelGGL((prefill_q4k<false, false, true>), dim3((unsigned)wgs), dim3(PF_THREADS), Pf::LDS, ctx->stream,
+                           pl, N, (int64_t)0, M, K, nullptr, nullptr, nullptr, nullptr, flags, nullptr);
+    }
+    return launch_check(ctx, "prefill_probe");
 }
 
 }  // namespace trhip

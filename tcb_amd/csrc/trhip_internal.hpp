@@ -362,6 +362,8 @@ int launch_prefill_q4k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int6
 // q6_k weights on the same tiles (prefill.hip), always exact.
 int launch_prefill_q6k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                        int64_t M, bool acc, const int8_t *qt, const float *dt, const uint8_t *bad);
+// The prefill kernels' inner loop alone on their real grid (prefill.hip): kind 0 q4_k exact, 1 q4_k fast, 2 q6_k.
+int launch_prefill_probe(trhip_ctx *ctx, int kind, int64_t M, int64_t N, int64_t K);
 int launch_mfma_probe(trhip_ctx *ctx, int valu_per_mfma, int waves_per_simd, int64_t iters);
 // Fast-mode q4_k product for 1 <= M <= 16 activation rows in one launch (rows16.hip); swi as in
 // launch_gemm_rows_fast. Returns -1 (nothing launched) where it does not apply.

@@ -1358,3 +1358,17 @@ def test_mfma_probe(backend):
     assert L.trhip_mfma_probe(backend.ctx.h, 5, 2, 8) == 1
     assert L.trhip_mfma_probe(backend.ctx.h, 0, 5, 8) == 1
     backend.ctx.sync()
+
+
+def test_prefill_probe_runs_and_refuses(backend):
+    """trhip_prefill_probe runs the three inner loops on a prefill grid and refuses bad kinds and shapes."""
+    from tcb_amd import _lib
+    L = _lib.lib()
+    h = backend.ctx.h
+    for kind in (0, 1, 2):
+        assert L.trhip_prefill_probe(h, kind, 512, 14336, 4096) == 0
+    backend.ctx.sync()
+    assert L.trhip_prefill_probe(h, 3, 512, 14336, 4096) == 1
+    assert L.trhip_prefill_probe(h, 1, 512, 14336, 4000) == 1
+    assert L.trhip_prefill_probe(h, 1, 0, 14336, 4096) == 1
+    backend.ctx.sync()
