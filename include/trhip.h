@@ -12,8 +12,9 @@
  *    serialized by the caller (the reference takes one backend lock per call,
  *    gpu/gpu.go:211-232). Work is asynchronous until trhip_sync / trhip_d2h.
  *  - Weights are [N, K] quantized rows (blocks along K), activations x are fp32 [M, K]
- *    row-major, outputs c are fp32 [M, N] row-major; x and c are device pointers from
- *    trhip_alloc (or any device allocation on the context's device).
+ *    row-major, outputs c are fp32 [M, N] row-major (f16 or bf16 either side through
+ *    trhip_gemm_q_typed); x and c are device pointers from trhip_alloc (or any device
+ *    allocation on the context's device).
  */
 #ifndef TRHIP_H
 #define TRHIP_H
@@ -46,6 +47,9 @@ enum { TRHIP_Q8 = 1, TRHIP_Q4 = 2, TRHIP_Q4K = 3, TRHIP_Q6K = 4 };
  * FAST:  per-sub-block factored sums; within 1e-5 (q8_0, q4_0) or 1e-4 (q4_k, q6_k) of EXACT by
  *        |a - b| / (1 + |b|), not bit-identical. */
 enum { TRHIP_MODE_EXACT = 0, TRHIP_MODE_FAST = 1 };
+
+/* Element types of activations and outputs for trhip_gemm_q_typed (fp32 everywhere else). */
+enum { TRHIP_F32 = 0, TRHIP_F16 = 1, TRHIP_BF16 = 2 };
 
 typedef struct trhip_ctx trhip_ctx;
 typedef struct trhip_wstore trhip_wstore;
@@ -144,6 +148,16 @@ int trhip_wstore_to_raw(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int
  * (gpu/kernel_quant_gemv.go:33-84, gpu/backend_quant.go:43-134). */
 int trhip_gemm_q(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x,
                  float *c, int64_t M, int64_t K, int accumulate, int mode);
+
+/* trhip_gemm_q with 16-bit activations and / or outputs (xtype, ctype: TRHIP_F32, TRHIP_F16, TRHIP_BF16; x holds
+ * M*K and c M*N elements of their type), as the reference's quantGemm takes them (gpu/backend_quant.go:41-45,
+ * gpu/backend_memory.go:41-52, 98-115): x is widened to fp32 exactly, the product is trhip_gemm_q's in fp32 (c
+ * widened first when accumulating), and c is rounded to its type once, to nearest even (tensor/cpu_dtype.go:73-123:
+ * NaN stays a quiet NaN, f16 overflows to Inf). Bit-identical to widening x, calling trhip_gemm_q and rounding its
+ * result. The batch-1 fast GEMV with x and c of one 16-bit type reads and writes them directly (x 8-byte and c
+ * 2-byte aligned); other cases go through fp32 copies in a workspace of the context. */
+int trhip_gemm_q_typed(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const void *x, int xtype,
+                       void *c, int ctype, int64_t M, int64_t K, int accumulate, int mode);
 
 /* ActQuantGemmer.GemmActQuant (tensor/matmul.go:59-61, tensor/cpu_dtype.go:438-446 ->
  * tensor/cpu_quant_q8.go:125-259): x rows are quantized on the device to Q8 blocks of the

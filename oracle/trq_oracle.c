@@ -53,6 +53,46 @@ float trq_f16_to_f32(uint16_t h) {
 
 static float fp16(const uint8_t *p) { return trq_f16_to_f32(le16(p)); } /* quant.go:136 */
 
+/* 16-bit activations and outputs (the typed matmul): cpu_dtype.go:73-80 (f32ToBF16), :83 (bf16ToF32), :87-123
+ * (f32ToF16), :125-145 (f16ToF32, trq_f16_to_f32 above). type 1 = f16, 2 = bf16. */
+static uint16_t f32_to_bf16(float f) {
+    uint32_t b = f32_bits(f);
+    if ((b & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((b >> 16) | 0x0040u); /* NaN, quieted */
+    b += 0x7FFFu + ((b >> 16) & 1u);                                            /* to nearest even */
+    return (uint16_t)(b >> 16);
+}
+
+static uint16_t f32_to_f16(float f) {
+    const uint32_t b = f32_bits(f);
+    const uint16_t sign = (uint16_t)((b >> 16) & 0x8000u);
+    const int ex = (int)((b >> 23) & 0xFFu);
+    uint32_t man = b & 0x7FFFFFu;
+    if (ex == 0xFF) return man ? (uint16_t)(sign | 0x7E00u | (man >> 13)) : (uint16_t)(sign | 0x7C00u);
+    const int e = ex - 127 + 15;
+    if (e >= 0x1F) return (uint16_t)(sign | 0x7C00u);
+    if (e <= 0) { /* subnormal or zero: the significand with its hidden bit, shifted */
+        if (e < -10) return sign;
+        man |= 0x800000u;
+        const unsigned sh = (unsigned)(14 - e);
+        uint32_t q = man >> sh;
+        const uint32_t rest = man & ((1u << sh) - 1u), half = 1u << (sh - 1);
+        if (rest > half || (rest == half && (q & 1u))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t h = ((uint32_t)e << 10) | (man >> 13);
+    const uint32_t rest = man & 0x1FFFu;
+    if (rest > 0x1000u || (rest == 0x1000u && (h & 1u))) h++;
+    return (uint16_t)(sign | h);
+}
+
+void trq_round16(int type, const float *src, uint16_t *dst, size_t n) {
+    for (size_t i = 0; i < n; i++) dst[i] = type == 2 ? f32_to_bf16(src[i]) : f32_to_f16(src[i]);
+}
+
+void trq_widen16(int type, const uint16_t *src, float *dst, size_t n) {
+    for (size_t i = 0; i < n; i++) dst[i] = type == 2 ? bits_f32((uint32_t)src[i] << 16) : trq_f16_to_f32(src[i]);
+}
+
 /* quant.go:158-163 */
 void trq_q4k_scale(int j, const uint8_t *q, uint8_t *sc, uint8_t *m) {
     if (j < 4) {

@@ -23,6 +23,9 @@
  *   trq_dot_q4q8/_q4kq8/_q6kq8        integer parts vs brute-force int64 from dequantized codes;
  *                                     float epilogue vs the float64 closeness bound of
  *                                     cpu_quant_q8_test.go:84
+ *   trq_round16 / trq_widen16         the reference's known answers (dtype_test.go:16-88), the round trip
+ *                                     of every 16-bit pattern, numpy's IEEE float16 rounding, nearest-even
+ *                                     bf16 by exhaustive neighbour comparison
  */
 #ifndef TRQ_ORACLE_H
 #define TRQ_ORACLE_H
@@ -42,6 +45,10 @@ int trq_block_bytes(int dt);
 
 /* cpu_dtype.go:126-145 (f16ToF32): exact, incl. subnormals and NaN payload. */
 float trq_f16_to_f32(uint16_t h);
+/* 16-bit activations and outputs, type 1 = float16, 2 = bfloat16: cpu_dtype.go:73-145 (rounding to nearest even,
+ * NaN quieted; widening exact). */
+void trq_round16(int type, const float *src, uint16_t *dst, size_t n);
+void trq_widen16(int type, const uint16_t *src, float *dst, size_t n);
 
 /* quant.go:158-163 (q4kScale). */
 void trq_q4k_scale(int j, const uint8_t *scales12, uint8_t *sc, uint8_t *m);

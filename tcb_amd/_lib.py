@@ -47,6 +47,7 @@ SIGNATURES = [
     ("trhip_wstore_to_raw", INT, [P, P, I64, I64, P]),
     ("trhip_wstore_concat", INT, [P, P, INT, ctypes.POINTER(P)]),
     ("trhip_gemm_q", INT, [P, P, I64, I64, P, P, I64, I64, INT, INT]),
+    ("trhip_gemm_q_typed", INT, [P, P, I64, I64, P, INT, P, INT, I64, I64, INT, INT]),
     ("trhip_gemm_q_actq", INT, [P, P, I64, I64, P, P, I64, I64, INT]),
     ("trhip_gemm_q_actq_noalloc", INT, [P, P, I64, I64, P, P, I64, I64, INT]),
     ("trhip_gemm_q_actq_mode", INT, [P, P, I64, I64, P, P, I64, I64, INT, INT]),
@@ -65,6 +66,7 @@ SIGNATURES = [
 OK, ERR_INVALID, ERR_OOM, ERR_HIP, ERR_LAUNCH, ERR_UNSUPPORTED, ERR_NO_DEVICE, ERR_BAD_SCALE = range(8)
 Q8, Q4, Q4K, Q6K = 1, 2, 3, 4
 MODE_EXACT, MODE_FAST = 0, 1
+F32, F16, BF16 = 0, 1, 2
 KNOB_KL, KNOB_FAST_Q4K, KNOB_EXACT_ROWS, KNOB_EXACT_LANES, KNOB_ACTQ_TM, KNOB_ROWS16, KNOB_KL_GRID = 1, 2, 3, 4, 5, 6, 7
 
 

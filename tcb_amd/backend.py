@@ -227,6 +227,12 @@ class QuantBackend:
     def GemmSet(self, M, N, K, a, w, c, row0=0, mode=MODE_EXACT):
         _check(_lib.lib().trhip_gemm_q(self.ctx.h, w.h, row0, N, _ptr(a), _ptr(c), M, K, 0, mode), self.ctx.h)
 
+    def GemmTyped(self, M, N, K, a, atype, w, c, ctype, row0=0, accumulate=False, mode=MODE_EXACT):
+        """Gemm / GemmSet with 16-bit activations or outputs (atype, ctype: F32, F16, BF16): a widened to fp32, the
+        fp32 product, c rounded once (gpu/backend_quant.go:41-45)."""
+        _check(_lib.lib().trhip_gemm_q_typed(self.ctx.h, w.h, row0, N, _ptr(a), atype, _ptr(c), ctype, M, K,
+                                             1 if accumulate else 0, mode), self.ctx.h)
+
     def GemmActQuant(self, M, N, K, a, w, c, row0=0, accumulate=True, mode=MODE_EXACT):
         """ActQuantGemmer.GemmActQuant (tensor/matmul.go:59-61); mode=MODE_FAST fuses the fp32 epilogue over the same
         exact integer block sums (trhip_gemm_q_actq_mode)."""

@@ -14,7 +14,8 @@ OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libtrhip.so")
 
 SOURCES = ["api.hip", "wstore.hip", "gemv.hip", "gemv_fast.hip", "gemm_rows.hip", "actq.hip", "actq_mfma.hip",
-           "swiglu.hip", "probe.hip", "prefill.hip", "rows16.hip", "actq6.hip", "actq4.hip"]
+           "swiglu.hip", "probe.hip", "prefill.hip", "rows16.hip", "actq6.hip", "actq4.hip",
+           "io16.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # -ffp-contract=off: no multiply-add is fused unless written as fmaf (bit-exact rounding order).

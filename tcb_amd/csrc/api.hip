@@ -68,6 +68,10 @@ void *workspace2(trhip_ctx *ctx, size_t bytes, int *status) {
     return grow(ctx, ctx->ws2, ctx->ws2_bytes, bytes, status);
 }
 
+void *workspace3(trhip_ctx *ctx, size_t bytes, int *status) {
+    return grow(ctx, ctx->ws3, ctx->ws3_bytes, bytes, status);
+}
+
 // Raise a kernel's dynamic-LDS cap on the context's device to at least `bytes`. The largest size granted so far is
 // kept per (device, kernel): a later call that needs more raises the cap again, one that needs less keeps it.
 int allow_dyn_lds(trhip_ctx *ctx, const void *fn, size_t bytes, const char *what) {
@@ -286,6 +290,7 @@ int trhip_destroy(trhip_ctx *ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->ws) (void)hipFree(ctx->ws);
     if (ctx->ws2) (void)hipFree(ctx->ws2);
+    if (ctx->ws3) (void)hipFree(ctx->ws3);
     if (ctx->arrivals) (void)hipFree(ctx->arrivals);
     for (void *p : ctx->retired) (void)hipFree(p);
     if (ctx->idx_host) (void)hipHostFree(ctx->idx_host);
@@ -834,6 +839,55 @@ int trhip_gemm_q(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N,
     if (mode == TRHIP_MODE_FAST && ((w->dtype == TRHIP_Q4K && M > 4) || (w->dtype == TRHIP_Q6K && M > 1)))
         return launch_gemm_rows_fast(ctx, w, row0, N, x, c, M, accumulate != 0);
     return launch_gemm_rows(ctx, w, row0, N, x, c, M, accumulate != 0);
+}
+
+int trhip_gemm_q_typed(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const void *x, int xtype,
+                       void *c, int ctype, int64_t M, int64_t K, int accumulate, int mode) {
+    if (!ctx || !w) return TRHIP_ERR_INVALID;
+    auto ok_type = [](int t) { return t == TRHIP_F32 || t == TRHIP_F16 || t == TRHIP_BF16; };
+    if (!ok_type(xtype) || !ok_type(ctype)) return fail(ctx, TRHIP_ERR_INVALID, "gemm_q_typed: bad element type");
+    if (xtype == TRHIP_F32 && ctype == TRHIP_F32)
+        return trhip_gemm_q(ctx, w, row0, N, static_cast<const float *>(x), static_cast<float *>(c), M, K, accumulate, mode);
+    if (M < 0 || N < 0 || row0 < 0 || row0 + N > w->N || K != w->K)
+        return fail(ctx, TRHIP_ERR_INVALID, "gemm_q_typed: shape does not match the store");
+    if (mode != TRHIP_MODE_EXACT && mode != TRHIP_MODE_FAST) return fail(ctx, TRHIP_ERR_INVALID, "gemm_q_typed: bad mode");
+    if (M == 0 || N == 0) return TRHIP_OK;
+    if (!c || (K != 0 && !x)) return fail(ctx, TRHIP_ERR_INVALID, "gemm_q_typed: null x or c");
+    DevGuard g(ctx);
+    const size_t cb = ctype == TRHIP_F32 ? 4 : 2;
+    if (K == 0) {  // empty sum (gpu/backend_quant.go:51-56): c unchanged, or zeroed (+0 in every type)
+        if (accumulate) return TRHIP_OK;
+        if (ctype == TRHIP_F32) return zero_f32(ctx, static_cast<float *>(c), M * N);
+        return fill_bytes(ctx, c, 0, (size_t)(M * N) * cb);
+    }
+    // the decode GEMV with 16-bit x and c of one type: read and written directly by the K-across-lanes kernel
+    if (M == 1 && mode == TRHIP_MODE_FAST && xtype == ctype && reinterpret_cast<uintptr_t>(x) % 8 == 0 &&
+        reinterpret_cast<uintptr_t>(c) % 2 == 0) {
+        const int r = launch_gemv_fast_io(ctx, w, row0, N, x, c, accumulate != 0, xtype);
+        if (r != -1) return r;
+    }
+    // otherwise the reference's own sequence (gpu/backend_memory.go:41-52, 98-115): x widened to fp32, c widened when
+    // accumulating, the fp32 operator, c rounded once
+    const size_t xbytes = xtype == TRHIP_F32 ? 0 : (size_t)(M * K) * sizeof(float);
+    const size_t o_c = (xbytes + 255) / 256 * 256;
+    const size_t cbytes = ctype == TRHIP_F32 ? 0 : (size_t)(M * N) * sizeof(float);
+    int st = TRHIP_OK;
+    uint8_t *ws = static_cast<uint8_t *>(workspace3(ctx, o_c + cbytes, &st));
+    if (!ws) return st;
+    const float *x32 = static_cast<const float *>(x);
+    if (xtype != TRHIP_F32) {
+        if ((st = launch_widen16(ctx, static_cast<const uint16_t *>(x), reinterpret_cast<float *>(ws), M * K, xtype)))
+            return st;
+        x32 = reinterpret_cast<const float *>(ws);
+    }
+    float *c32 = static_cast<float *>(c);
+    if (ctype != TRHIP_F32) {
+        c32 = reinterpret_cast<float *>(ws + o_c);
+        if (accumulate && (st = launch_widen16(ctx, static_cast<const uint16_t *>(c), c32, M * N, ctype))) return st;
+    }
+    if ((st = trhip_gemm_q(ctx, w, row0, N, x32, c32, M, K, accumulate, mode))) return st;
+    if (ctype != TRHIP_F32) return launch_round16(ctx, c32, static_cast<uint16_t *>(c), M * N, ctype);
+    return TRHIP_OK;
 }
 
 int trhip_swiglu(trhip_ctx *ctx, const float *gu, int64_t M, int64_t I, float *out) {

@@ -297,9 +297,12 @@ struct KlRow<kQ6K> {  // ql pieces t at 32t + 16n, qh pieces at 16t + 8n, the la
 // swiglu_kernel gates them.
 // SKIP: the grid has more row groups than RPW-row groups need, so a group's last slots may lie past its rows; they
 // still load (a re-read of the last row, which keeps every wait count fixed) but skip the arithmetic
-template <int DT, bool ACC, int WAVES, int KS, int PD, int RPW, bool SWI = false, bool SKIP = false>
-__global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const float *__restrict__ x,
-                                                      float *__restrict__ c, int64_t N, int64_t row0) {
+// IO: TRHIP_F32, or TRHIP_F16 / TRHIP_BF16 for 16-bit x read and 16-bit c written directly (widened exactly and
+// rounded once, as the typed entry point's staged path does; not with SWI).
+template <int DT, bool ACC, int WAVES, int KS, int PD, int RPW, bool SWI = false, bool SKIP = false, int IO = TRHIP_F32>
+__global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const void *__restrict__ xv,
+                                                      void *__restrict__ cv, int64_t N, int64_t row0) {
+    static_assert(IO == TRHIP_F32 || !SWI, "the gated output is fp32");
     static_assert(!(SWI && ACC), "the gated output is set, not accumulated");
     static_assert(!SWI || RPW % 2 == 0, "slots come in gate / up pairs");
     constexpr int RG = WAVES / KS;
@@ -320,12 +323,23 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const floa
     const int g = lane & 3, b = pb0 + (K4 ? (lane >> 2) : 2 * lane);
     const bool active = b < pb1;
     const int bc = active ? b : (pb0 < nb ? pb0 : (K4 ? nb - 1 : nb - 2));  // inactive lanes read valid blocks
-    const float4 *x4 = reinterpret_cast<const float4 *>(x + (K4 ? 256 * (int64_t)bc + 64 * g : 32 * (int64_t)bc));
+    // this lane's x, four elements at a time from element xe0 (widened exactly when 16-bit)
+    const int64_t xe0 = K4 ? 256 * (int64_t)bc + 64 * g : 32 * (int64_t)bc;
+    auto x4 = [&](int i) -> float4 {
+        if constexpr (IO == TRHIP_F32) {
+            return reinterpret_cast<const float4 *>(static_cast<const float *>(xv) + xe0)[i];
+        } else {
+            const uint2 h = reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(xv) + xe0)[i];
+            return make_float4(h16_to_f32(h.x & 0xFFFFu, IO), h16_to_f32(h.x >> 16, IO), h16_to_f32(h.y & 0xFFFFu, IO),
+                               h16_to_f32(h.y >> 16, IO));
+        }
+    };
+    float *c = static_cast<float *>(cv);  // (IO == TRHIP_F32)
     // issue order: this wave's columns of x (cache-resident), then the first PD rows, so that waiting for x
     // leaves the rows in flight
     float4 xraw[CPW];
 #pragma unroll
-    for (int i = 0; i < CPW; i++) xraw[i] = x4[rg * CPW + i];
+    for (int i = 0; i < CPW; i++) xraw[i] = x4(rg * CPW + i);
     const int k0 = (2 * g) & 3, k1 = k0 + 1;
     // q4_k: header of the lane's block, and qs 16-byte pieces g and g + 4 of it; q8_0 / q4_0: the two blocks'
     // codes (64 / 32 contiguous bytes) and their two fp16 scales (one aligned dword)
@@ -505,8 +519,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const floa
                 for (int kk = 0; kk < 2; kk++)
 #pragma unroll
                     for (int k = 0; k < 8; k++) {
-                        const float4 xv = x4[8 * kk + k];
-                        const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
+                        const float4 xq = x4(8 * kk + k);
+                        const float xs[4] = {xq.x, xq.y, xq.z, xq.w};
                         const float ds = d6 * (float)(int8_t)((rw.sc >> (8 * (2 * kk + (k >> 2)))) & 0xFF);
 #pragma unroll
                         for (int e = 0; e < 4; e++)
@@ -553,7 +567,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const floa
                 a = 0.0f;
 #pragma unroll
                 for (int k = 0; k < 8; k++) {
-                    const float4 xl = x4[k], xh = x4[8 + k];
+                    const float4 xl = x4(k), xh = x4(8 + k);
                     const uint32_t lo = qw[k] & 0x0F0F0F0Fu, hi = (qw[k] >> 4) & 0x0F0F0F0Fu;
                     const float xlv[4] = {xl.x, xl.y, xl.z, xl.w}, xhv[4] = {xh.x, xh.y, xh.z, xh.w};
 #pragma unroll
@@ -617,8 +631,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const floa
                     const float dd = hf ? d1 : d0;
 #pragma unroll
                     for (int k = 0; k < 8; k++) {
-                        const float4 xv = x4[8 * hf + k];
-                        const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
+                        const float4 xq = x4(8 * hf + k);
+                        const float xs[4] = {xq.x, xq.y, xq.z, xq.w};
                         const uint32_t wq = qw[8 * hf + k];
 #pragma unroll
                         for (int t = 0; t < 4; t++) {
@@ -651,7 +665,14 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const floa
             if (part == 0 && (lane & 15) == 0 && j < nv) c[gw + (int64_t)j * G] = silu_ref(sum) * up;
         } else {
             const int64_t r = gw + (int64_t)(i0 + ri) * G;
-            if (part == 0 && (lane & 7) == 0 && (uint32_t)(i0 + ri) < nv) c[r] = ACC ? c[r] + sum : sum;
+            if (part == 0 && (lane & 7) == 0 && (uint32_t)(i0 + ri) < nv) {
+                if constexpr (IO == TRHIP_F32) {
+                    c[r] = ACC ? c[r] + sum : sum;
+                } else {  // c widened, the sum added in fp32, rounded once
+                    uint16_t *c16 = static_cast<uint16_t *>(cv);
+                    c16[r] = (uint16_t)f32_to_h16(ACC ? h16_to_f32(c16[r], IO) + sum : sum, IO);
+                }
+            }
         }
     }
 }
@@ -663,8 +684,8 @@ __host__ __forceinline__ bool kl_fits(int dt, int64_t nb, int ks) {
     return nb % 2 == 0 && ((nb + ks - 1) / ks + 1) / 2 * 2 <= 128;
 }
 
-template <int DT, int WAVES, int KS, int PD, int RPW, bool SWI = false>
-int run_kl(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c, bool acc) {
+template <int DT, int WAVES, int KS, int PD, int RPW, bool SWI = false, int IO = TRHIP_F32>
+int run_kl(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const void *x, void *c, bool acc) {
     constexpr int RG = WAVES / KS;
     if (!kl_fits(DT, w->nb, KS)) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv_kl: K parts too long for the lanes of a wave");
     constexpr int OPW = SWI ? RPW / 2 : RPW;  // outputs per row group (SWI: two rows per output)
@@ -691,10 +712,10 @@ int run_kl(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const
         return skip ? go(gemv_kl<DT, false, WAVES, KS, PD, RPW, true, true>)
                     : go(gemv_kl<DT, false, WAVES, KS, PD, RPW, true, false>);
     if (acc)
-        return skip ? go(gemv_kl<DT, true, WAVES, KS, PD, RPW, false, true>)
-                    : go(gemv_kl<DT, true, WAVES, KS, PD, RPW, false, false>);
-    return skip ? go(gemv_kl<DT, false, WAVES, KS, PD, RPW, false, true>)
-                : go(gemv_kl<DT, false, WAVES, KS, PD, RPW, false, false>);
+        return skip ? go(gemv_kl<DT, true, WAVES, KS, PD, RPW, false, true, IO>)
+                    : go(gemv_kl<DT, true, WAVES, KS, PD, RPW, false, false, IO>);
+    return skip ? go(gemv_kl<DT, false, WAVES, KS, PD, RPW, false, true, IO>)
+                : go(gemv_kl<DT, false, WAVES, KS, PD, RPW, false, false, IO>);
 }
 
 template <int D, int WAVES, int KS, int R>
@@ -835,6 +856,53 @@ int launch_gemv_fast(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_
         return run_q4k<2, 4, 2, 1>(ctx, w, row0, N, x, c, acc);
     }
     return launch_gemv(ctx, w, row0, N, x, c, acc, TRHIP_MODE_EXACT);
+}
+
+// 16-bit x and c on the K-across-lanes kernel: the same launch shapes launch_gemv_fast takes for each dtype and store
+// shape (so the row sums are those of the fp32 call on the widened x), kNotTaken where it would take another kernel
+// or a launch shape is forced on the context.
+namespace {
+template <int IO>
+int gemv_fast_io(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const void *x, void *c, bool acc) {
+    if (ctx->force_kl || ctx->force_fast_q4k || ctx->kl_min_wgs) return kNotTaken;
+    switch (w->dtype) {
+    case kQ4K:
+        if (w->nb >= 8 && w->nb <= 16)
+            return N >= 10240 ? run_kl<kQ4K, 4, 1, 4, 16, false, IO>(ctx, w, row0, N, x, c, acc)
+                              : run_kl<kQ4K, 4, 1, 4, 8, false, IO>(ctx, w, row0, N, x, c, acc);
+        if (w->nb > 16 && kl_fits(kQ4K, w->nb, 4) && N >= 4096)
+            return run_kl<kQ4K, 8, 4, 4, 8, false, IO>(ctx, w, row0, N, x, c, acc);
+        return kNotTaken;
+    case kQ6K:
+        if (kl_fits(kQ6K, w->nb, 1))
+            return N >= 10240 ? run_kl<kQ6K, 4, 1, 4, 16, false, IO>(ctx, w, row0, N, x, c, acc)
+                              : run_kl<kQ6K, 4, 1, 4, 8, false, IO>(ctx, w, row0, N, x, c, acc);
+        if (kl_fits(kQ6K, w->nb, 4)) return run_kl<kQ6K, 8, 4, 4, 8, false, IO>(ctx, w, row0, N, x, c, acc);
+        return kNotTaken;
+    case kQ8:
+    case kQ4:
+        if (kl_fits(w->dtype, w->nb, 1)) {
+            if (w->dtype == kQ8)
+                return N >= 10240 ? run_kl<kQ8, 4, 1, 4, 16, false, IO>(ctx, w, row0, N, x, c, acc)
+                                  : run_kl<kQ8, 4, 1, 4, 8, false, IO>(ctx, w, row0, N, x, c, acc);
+            return N >= 10240 ? run_kl<kQ4, 4, 1, 4, 16, false, IO>(ctx, w, row0, N, x, c, acc)
+                              : run_kl<kQ4, 4, 1, 4, 8, false, IO>(ctx, w, row0, N, x, c, acc);
+        }
+        if (kl_fits(w->dtype, w->nb, 4))
+            return w->dtype == kQ8 ? run_kl<kQ8, 8, 4, 4, 8, false, IO>(ctx, w, row0, N, x, c, acc)
+                                   : run_kl<kQ4, 8, 4, 4, 8, false, IO>(ctx, w, row0, N, x, c, acc);
+        return kNotTaken;
+    }
+    return kNotTaken;
+}
+}  // namespace
+
+int launch_gemv_fast_io(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const void *x, void *c,
+                        bool acc, int io) {
+    if (N == 0) return TRHIP_OK;
+    if (io == TRHIP_F16) return gemv_fast_io<TRHIP_F16>(ctx, w, row0, N, x, c, acc);
+    if (io == TRHIP_BF16) return gemv_fast_io<TRHIP_BF16>(ctx, w, row0, N, x, c, acc);
+    return kNotTaken;
 }
 
 }  // namespace trhip

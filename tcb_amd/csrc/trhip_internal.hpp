@@ -64,6 +64,44 @@ __device__ __forceinline__ float f16_to_f32(uint16_t h) {  // exact for finite v
     return (float)__builtin_bit_cast(_Float16, h);
 }
 
+// 16-bit activation / output formats of the typed entry point (TRHIP_F16, TRHIP_BF16), widened and rounded as the
+// reference does. Widening is exact: bf16ToF32 (tensor/cpu_dtype.go:83), f16ToF32 (:125-145, a NaN keeps its
+// payload). Rounding to nearest even with the reference's NaN and overflow rules: f32ToBF16 (:73-80, NaN quieted by
+// or-ing 0x0040), f32ToF16 (:87-123, NaN quieted as 0x7E00 | payload >> 13; 65520 and above to Inf; subnormals
+// rounded from the shifted significand).
+__device__ __forceinline__ float h16_to_f32(uint32_t h, int io) {
+    if (io == TRHIP_BF16) return __uint_as_float(h << 16);
+    if (((h >> 10) & 0x1Fu) == 0x1Fu) return __uint_as_float(((h & 0x8000u) << 16) | 0x7F800000u | ((h & 0x3FFu) << 13));
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);  // finite values, subnormals included: exact
+}
+__device__ __forceinline__ uint32_t f32_to_h16(float f, int io) {
+    uint32_t b = __float_as_uint(f);
+    if (io == TRHIP_BF16) {
+        if ((b & 0x7FFFFFFFu) > 0x7F800000u) return ((b >> 16) | 0x0040u) & 0xFFFFu;
+        b += 0x7FFFu + ((b >> 16) & 1u);
+        return b >> 16;
+    }
+    const uint32_t sign = (b >> 16) & 0x8000u;
+    const int us = (int)((b >> 23) & 0xFFu);
+    uint32_t ak = b & 0x7FFFFFu;
+    if (us == 0xFF) return ak ? (sign | 0x7E00u | (ak >> 13)) : (sign | 0x7C00u);
+    const int e = us - 127 + 15;
+    if (e >= 0x1F) return sign | 0x7C00u;
+    if (e <= 0) {
+        if (e < -10) return sign;
+        ak |= 0x800000u;
+        const uint32_t sh = (uint32_t)(14 - e);
+        uint32_t m = ak >> sh;
+        const uint32_t rest = ak & ((1u << sh) - 1u), half = 1u << (sh - 1);
+        if (rest > half || (rest == half && (m & 1u))) m++;
+        return sign | m;
+    }
+    uint32_t h = ((uint32_t)e << 10) | (ak >> 13);
+    const uint32_t rest = ak & 0x1FFFu;
+    if (rest > 0x1000u || (rest == 0x1000u && (h & 1u))) h++;
+    return sign | h;
+}
+
 // Hide a value from the optimizer (no instruction is emitted). Used on a dword-wide nibble mask so the
 // compiler keeps one v_and_b32 per four codes and converts each byte with one v_cvt_f32_ubyte{k},
 // instead of folding the mask into four per-byte bit-field extracts.
@@ -266,6 +304,10 @@ struct trhip_ctx {
     // (the merged gate_up output of trhip_gemm_q_swiglu).
     void *ws2 = nullptr;
     size_t ws2_bytes = 0;
+    // A third for the fp32 copies of 16-bit activations and outputs (trhip_gemm_q_typed), which live across the call
+    // of the fp32 operator that uses the others.
+    void *ws3 = nullptr;
+    size_t ws3_bytes = 0;
     // Workspace buffers replaced by a larger one while instantiated graphs of this context exist: their kernel
     // nodes may still hold the old addresses, so the buffers are freed only when the last graph is destroyed
     // (or with the context).
@@ -362,6 +404,15 @@ int launch_prefill_q4k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int6
 // q6_k weights on the same tiles (prefill.hip), always exact.
 int launch_prefill_q6k(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
                        int64_t M, bool acc, const int8_t *qt, const float *dt, const uint8_t *bad);
+// 16-bit activations / outputs (io16.hip): dst[i] = widen(src[i]) and dst[i] = round(src[i]) for n elements.
+int launch_widen16(trhip_ctx *ctx, const uint16_t *src, float *dst, int64_t n, int io);
+int launch_round16(trhip_ctx *ctx, const float *src, uint16_t *dst, int64_t n, int io);
+// The fast K-across-lanes GEMV reading 16-bit x and writing 16-bit c (io) directly (gemv_fast.hip), or -1 when the
+// store's shape does not take that kernel.
+int launch_gemv_fast_io(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const void *x, void *c,
+                        bool acc, int io);
+void *workspace3(trhip_ctx *ctx, size_t bytes, int *status);
+
 // The prefill kernels' inner loop alone on their real grid (prefill.hip): kind 0 q4_k exact, 1 q4_k fast, 2 q6_k.
 int launch_prefill_probe(trhip_ctx *ctx, int kind, int64_t M, int64_t N, int64_t K);
 int launch_mfma_probe(trhip_ctx *ctx, int valu_per_mfma, int waves_per_simd, int64_t iters);

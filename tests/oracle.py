@@ -143,6 +143,22 @@ def block_isums(dt, w_row, q, bs):
     return isum, msum
 
 
+def round16(t, x):
+    """float32 array -> uint16 patterns of type t (1 = f16, 2 = bf16), cpu_dtype.go:73-123."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    out = np.zeros(x.size, np.uint16)
+    lib().trq_round16(t, _p(x), _p(out), SZ(x.size))
+    return out
+
+
+def widen16(t, h):
+    """uint16 patterns of type t -> float32 (exact), cpu_dtype.go:83, :125-145."""
+    h = np.ascontiguousarray(h, np.uint16).reshape(-1)
+    out = np.zeros(h.size, np.float32)
+    lib().trq_widen16(t, _p(h), _p(out), SZ(h.size))
+    return out
+
+
 def quant_zero_raw(dt, n):
     out = np.zeros(n // BLOCK[dt][0] * BLOCK[dt][1], np.uint8)
     lib().trq_quant_zero_raw(dt, n, _p(out))

@@ -482,3 +482,73 @@ def test_swiglu_gate_is_first_half():
     u = np.full((M, I), 2.0, np.float32)
     out = O.swiglu(np.concatenate([g, u], axis=1), M, I)
     assert np.array_equal(out, (O.silu(g).reshape(M, I) * np.float32(2)).astype(np.float32))
+
+
+# ---- 16-bit activations and outputs: the reference's rounding and widening (tensor/cpu_dtype.go:73-145)
+
+def _f32(b):
+    return np.array([b], np.uint32).view(np.float32)[0]
+
+
+BF16_EDGES = [  # tensor/dtype_test.go:17-34
+    (0.0, 0x0000), (-0.0, 0x8000), (1.0, 0x3F80), (-2.0, 0xC000),
+    (1 + 1.0 / 256, 0x3F80), (1 + 3.0 / 256, 0x3F82), (1 + 1.0 / 256 + 1.0 / (1 << 20), 0x3F81),
+    (_f32(0x7F7FFFFF), 0x7F80), (-_f32(0x7F7FFFFF), 0xFF80), (_f32(0x7F7F0000), 0x7F7F),
+    (np.inf, 0x7F80), (-np.inf, 0xFF80), (_f32(0x00010000), 0x0001), (_f32(0x00008000), 0x0000),
+    (_f32(0x00018000), 0x0002)]
+F16_EDGES = [  # tensor/dtype_test.go:52-75
+    (0.0, 0x0000), (-0.0, 0x8000), (1.0, 0x3C00), (-2.0, 0xC000), (65504.0, 0x7BFF), (65519.0, 0x7BFF),
+    (65520.0, 0x7C00), (1e6, 0x7C00), (-1e6, 0xFC00), (1 + 1.0 / 2048, 0x3C00), (1 + 3.0 / 2048, 0x3C02),
+    (6.103515625e-05, 0x0400), (5.960464477539063e-08, 0x0001), (2.9802322387695312e-08, 0x0000),
+    (2.9802322387695312e-08 * 1.0001, 0x0001), (4.470348358154297e-08, 0x0001), (8.940696716308594e-08, 0x0002),
+    (6.097555160522461e-05, 0x03FF), (6.1005353927612305e-05, 0x0400), (1e-10, 0x0000), (-1e-10, 0x8000),
+    (np.inf, 0x7C00), (-np.inf, 0xFC00)]
+
+
+@pytest.mark.parametrize("t,cases", [(2, BF16_EDGES), (1, F16_EDGES)])
+def test_round16_reference_edges(t, cases):
+    """The reference's known answers for float32 -> bfloat16 / float16 (ties to even, overflow, subnormals)."""
+    x = np.array([c[0] for c in cases], np.float32)
+    want = np.array([c[1] for c in cases], np.uint16)
+    assert np.array_equal(O.round16(t, x), want)
+
+
+@pytest.mark.parametrize("t", [1, 2])
+def test_round16_nan_and_round_trip(t):
+    """NaN stays NaN (bfloat16: quieted by 0x0040, tensor/dtype_test.go:42-47); every non-NaN 16-bit pattern widens
+    exactly and rounds back to itself (tensor/dtype_test.go:91-100)."""
+    nans = np.array([0x7FC00000, 0x7F800001, 0xFFC00000, 0x7F80FFFF], np.uint32).view(np.float32)
+    h = O.round16(t, nans)
+    assert np.all(np.isnan(O.widen16(t, h)))
+    if t == 2:
+        assert np.all(h & 0x0040)
+    allbits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    wide = O.widen16(t, allbits)
+    keep = ~np.isnan(wide)
+    assert np.array_equal(O.round16(t, wide[keep]), allbits[keep])
+    if t == 1:  # the f16 widening agrees with numpy's for every non-NaN pattern
+        assert np.array_equal(wide[keep].view(np.uint32), allbits[keep].view(np.float16).astype(np.float32).view(np.uint32))
+
+
+def test_round16_nearest_even_on_random_floats():
+    """float16: numpy's IEEE conversion (round to nearest even) on finite values of every magnitude. bfloat16: the
+    result is the nearest of its neighbours, ties to the even pattern."""
+    rng = np.random.default_rng(3)
+    bits = rng.integers(0, 1 << 32, size=200000, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    x = x[np.isfinite(x)]
+    with np.errstate(over="ignore"):
+        assert np.array_equal(O.round16(1, x), x.astype(np.float16).view(np.uint16))
+    h = O.round16(2, x).astype(np.int64)
+    xd = x.astype(np.float64)
+    fin = np.abs(xd) < float(_f32(0x7F7F8000))  # below the bfloat16 overflow threshold
+    h, xd = h[fin], xd[fin]
+    inner = ((h & 0x7FFF) > 0) & ((h & 0x7FFF) < 0x7F7F)  # both neighbours are finite patterns of the same sign
+    h, xd = h[inner], xd[inner]
+    mag = h & 0x7FFF
+    sign = h & 0x8000
+    w = lambda m: O.widen16(2, (sign | m).astype(np.uint16)).astype(np.float64)
+    d0 = np.abs(xd - w(mag))
+    assert np.all(d0 <= np.abs(xd - w(mag + 1))) and np.all(d0 <= np.abs(xd - w(mag - 1)))
+    tie = (d0 == np.abs(xd - w(mag + 1))) | (d0 == np.abs(xd - w(mag - 1)))
+    assert np.all((mag[tie & (d0 > 0)] & 1) == 0)
