@@ -466,6 +466,21 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const void
                 c6[q][t] = -32 * sdg;
             }
     }
+    // q4_k: the high nibbles stay in place as the signed bytes (16 q - 128) = (w ^ 0x80) & 0xF0 (one v_bitop3), so
+    // their chains start at 128 times the high half's digit sums and end at exactly 16 sum q X; the lane's scale
+    // and min bytes are shifted to bytes 0 and 1 (shifts sa, sy, sm below) from header words chosen by g
+    int hc[3] = {0, 0, 0};
+    if constexpr (DT == kQ4K) {
+#pragma unroll
+        for (int t = 0; t < 3; t++) {
+            int sdg = 0;
+#pragma unroll
+            for (int k = 0; k < 8; k++) sdg = __builtin_amdgcn_sdot4(0x01010101, xd[1][k][t], sdg, false);
+            hc[t] = 128 * sdg;
+        }
+    }
+    const uint32_t sa = 16u * (g & 1), sy = sa + (g < 2 ? 0u : 2u), sm = sa + (g < 2 ? 0u : 4u);
+    const int exh = ex[1] - 4;  // the high half's sums are 16 times too large
 #pragma unroll
     for (int i0 = 0; i0 < RPW; i0 += 8) {
         float v[8];
@@ -530,25 +545,25 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const void
             } else if constexpr (DT == kQ4K) {
             const uint4 h = rw.h, q0 = rw.q0, q1 = rw.q1;
             const float d = f16_to_f32((uint16_t)(h.x & 0xFFFF)), dmin = f16_to_f32((uint16_t)(h.x >> 16));
-            uint32_t sc_lo, sc_hi, m_lo, m_hi;
-            q4k_scales(h.y, h.z, h.w, sc_lo, sc_hi, m_lo, m_hi);
-            const uint32_t scw = g < 2 ? sc_lo : sc_hi, mw = g < 2 ? m_lo : m_hi;
+            // scale and min of sub-blocks 2g and 2g + 1 unpacked into bytes 0 and 1 (tensor/quant.go:158-163): g < 2
+            // keeps six bits of scale word y / z, g >= 2 four bits of word w and the top two of y / z
+            const uint32_t xs = (g < 2 ? h.y : h.w) >> sa, xm = (g < 2 ? h.z : h.w) >> sm;
+            const uint32_t sc2 = (xs & 0x0F0Fu) | ((h.y >> sy) & 0x3030u), m2 = (xm & 0x0F0Fu) | ((h.z >> sy) & 0x3030u);
+            const float sc0 = ubyte_f(sc2, 0), sc1 = ubyte_f(sc2, 1), m0 = ubyte_f(m2, 0), m1 = ubyte_f(m2, 1);
             const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-            const float s0 = d * ubyte_f(scw, k0), n0 = -(dmin * ubyte_f(mw, k0));
-            const float s1 = d * ubyte_f(scw, k1), n1 = -(dmin * ubyte_f(mw, k1));
             int l0, l1, l2, h0, h1, h2;
             {
-                const int lo = (int)(qw[0] & 0x0F0F0F0Fu), hi = (int)((qw[0] >> 4) & 0x0F0F0F0Fu);
+                const int lo = (int)(qw[0] & 0x0F0F0F0Fu), hi = (int)((qw[0] ^ 0x80808080u) & 0xF0F0F0F0u);
                 l0 = sdot4_zero(lo, xd[0][0][0]);
                 l1 = sdot4_zero(lo, xd[0][0][1]);
                 l2 = sdot4_zero(lo, xd[0][0][2]);
-                h0 = sdot4_zero(hi, xd[1][0][0]);
-                h1 = sdot4_zero(hi, xd[1][0][1]);
-                h2 = sdot4_zero(hi, xd[1][0][2]);
+                h0 = sdot4_from(hi, xd[1][0][0], hc[0]);
+                h1 = sdot4_from(hi, xd[1][0][1], hc[1]);
+                h2 = sdot4_from(hi, xd[1][0][2], hc[2]);
             }
 #pragma unroll
             for (int k = 1; k < 8; k++) {
-                const int lo = (int)(qw[k] & 0x0F0F0F0Fu), hi = (int)((qw[k] >> 4) & 0x0F0F0F0Fu);
+                const int lo = (int)(qw[k] & 0x0F0F0F0Fu), hi = (int)((qw[k] ^ 0x80808080u) & 0xF0F0F0F0u);
                 l0 = __builtin_amdgcn_sdot4(lo, xd[0][k][0], l0, false);
                 l1 = __builtin_amdgcn_sdot4(lo, xd[0][k][1], l1, false);
                 l2 = __builtin_amdgcn_sdot4(lo, xd[0][k][2], l2, false);
@@ -556,12 +571,15 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const void
                 h1 = __builtin_amdgcn_sdot4(hi, xd[1][k][1], h1, false);
                 h2 = __builtin_amdgcn_sdot4(hi, xd[1][k][2], h2, false);
             }
-            // |l1| * 256 + |l0| < 2^24, so the first two digits add exactly, in 32-bit integers as in float
+            // |l1| * 256 + |l0| < 2^24, so the first two digits add exactly, in 32-bit integers as in float (the high
+            // half's, 16 times as large, too: a multiple of 16 below 2^28)
             const float pl = fmaf((float)l2, 65536.0f, (float)(l1 * 256 + l0));
             const float ph = fmaf((float)h2, 65536.0f, (float)(h1 * 256 + h0));
+            // d and dmin are applied before the 2^e scaling, so no partial overflows ahead of the sum itself
+            const float s0 = d * sc0, n0 = -(dmin * m0), s1 = d * sc1, n1 = -(dmin * m1);
             a = ldexpf(s0 * pl, ex[0]);
             a = fmaf(n0, sxl, a);
-            a = a + ldexpf(s1 * ph, ex[1]);
+            a = a + ldexpf(s1 * ph, exh);
             a = fmaf(n1, sxh, a);
             if (!fin) {  // Inf or NaN in this lane's x: dequantized values times x in float
                 a = 0.0f;

@@ -903,8 +903,8 @@ def test_gemv_kl_tolerance(backend, launch_shape, cfg, N, K, row0):
 
 @pytest.mark.parametrize("cfg", ["4,1,4,16", "8,4,4,8"])
 def test_gemv_kl_activation_range(backend, launch_shape, cfg):
-    """Fixed-point x is scaled per 32-element half: one huge element among tiny ones, an all-zero half, and
-    subnormal activations stay within tolerance (zero x gives zero rows)."""
+    """Fixed-point x is scaled per 32-element half: one huge element among tiny ones, an all-zero half, subnormal
+    activations and activations near 1e35 stay within tolerance (zero x gives zero rows)."""
     launch_shape(KNOB_KL, *map(int, cfg.split(",")))
     N, K = 64, 4096 if _kl_parts(cfg) == 1 else 14336
     raw = synth.quant_weights(Q4K, N, K, seed=8, outliers=0.01)
@@ -918,6 +918,7 @@ def test_gemv_kl_activation_range(backend, launch_shape, cfg):
     xs.append((rng.standard_normal(K) * 1e-40).astype(np.float32))  # subnormal
     xs.append(np.zeros(K, np.float32))
     xs.append((rng.standard_normal(K) * 1e30).astype(np.float32))
+    xs.append((rng.standard_normal(K) * 1e35).astype(np.float32))  # sums far from overflow, sc * X * 2^e near it
     for x in xs:
         xb, cb = backend.ctx.to_device(x), backend.ctx.alloc(N * 4)
         backend.GemmSet(1, N, K, xb, w, cb, mode=MODE_FAST)
