@@ -586,8 +586,13 @@ int launch_rows16(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N
         tpw = ctx->force_rows16 / 100 % 10;
         S = ctx->force_rows16 % 100;
     } else {  // one workgroup per CU, at most four slices (measured on the Llama shapes at M = 16)
-        tpw = 1;
-        const int64_t rt = (N + 63) / 64, cus = ctx->sm_count > 0 ? ctx->sm_count : 256;
+        // 128-row tiles where they still give three workgroups for four CUs: each block's activation record then
+        // serves twice the weight rows (28672x4096, M = 16, cold: 23.6 against 26.6 us; at 14336 rows the 112
+        // workgroups take 21.8 against 16.7). Further K slices cost their partial sums: 14336x4096 in two slices
+        // 19.4 against 16.7 us.
+        const int64_t cus = ctx->sm_count > 0 ? ctx->sm_count : 256;
+        tpw = 4 * ((N + 127) / 128) >= 3 * cus ? 2 : 1;
+        const int64_t rt = (N + 64 * tpw - 1) / (64 * tpw);
         S = (int)((cus + rt / 2) / rt);
         if (S > 4) S = 4;
     }
