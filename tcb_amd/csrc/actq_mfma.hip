@@ -875,7 +875,7 @@ __device__ __forceinline__ v8h q6_codes(const Q6Regs &r, int s) {
 }
 
 template <bool ACC>
-__global__ __launch_bounds__(FM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void fastm16_q6k(
+__global__ __launch_bounds__(FM_THREADS) __attribute__((amdgpu_waves_per_eu(3, 3))) void fastm16_q6k(
     const Planes p, int64_t N, int64_t row0, int64_t M, int64_t K, const float *__restrict__ x,
     const uint16_t *__restrict__ xh, const uint16_t *__restrict__ xl, const int *__restrict__ ex,
     const uint8_t *__restrict__ bad, int64_t bps, float *__restrict__ c, float *__restrict__ partial) {
