@@ -96,6 +96,51 @@ def test_check_quant_scales_large_inputs(dt):
                 assert bad.value == (min(seen) if seen else -1), (dt, bads, nbytes)
 
 
+def test_check_quant_scales_concurrent_and_forked():
+    """The host scan's worker pool serves one split at a time: scans from several threads at once all give the
+    first bad block, and a forked child (which has none of the pool's workers) scans on its own thread."""
+    import threading
+    from tcb_amd import _lib
+    lib = _lib.lib()
+    dt, size = 3, O.BLOCK[3][1]
+    nblk = (6 << 20) // size
+    raws, want = [], []
+    for i in range(6):
+        raw = np.zeros(nblk * size, np.uint8)
+        b = (i * 977 + 11) % nblk
+        raw[b * size + 2], raw[b * size + 3] = 0x00, 0x7E  # NaN dmin
+        raws.append(raw)
+        want.append(b)
+    got = [None] * len(raws)
+
+    def scan(i):
+        for _ in range(5):
+            bad = ctypes.c_int64(0)
+            assert lib.trhip_check_quant_scales(dt, raws[i].ctypes.data_as(ctypes.c_void_p), raws[i].size,
+                                                ctypes.byref(bad)) == 0
+            got[i] = bad.value
+
+    ts = [threading.Thread(target=scan, args=(i,)) for i in range(len(raws))]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join(60)
+    assert got == want
+    r, w = os.pipe()
+    pid = os.fork()
+    if pid == 0:  # child: scan, report, exit without running the parent's cleanup
+        bad = ctypes.c_int64(0)
+        lib.trhip_check_quant_scales(dt, raws[1].ctypes.data_as(ctypes.c_void_p), raws[1].size, ctypes.byref(bad))
+        os.write(w, str(bad.value).encode())
+        os._exit(0)
+    os.close(w)
+    import select
+    ready, _, _ = select.select([r], [], [], 60)
+    assert ready, "the forked child's scan did not finish"
+    assert int(os.read(r, 64)) == want[1]
+    os.waitpid(pid, 0)
+
+
 def test_missing_library_fails_loudly(tmp_path):
     from tcb_amd import _lib
     with pytest.raises(ImportError):
