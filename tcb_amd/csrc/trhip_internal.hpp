@@ -71,35 +71,25 @@ __device__ __forceinline__ float f16_to_f32(uint16_t h) {  // exact for finite v
 // rounded from the shifted significand).
 __device__ __forceinline__ float h16_to_f32(uint32_t h, int io) {
     if (io == TRHIP_BF16) return __uint_as_float(h << 16);
-    if (((h >> 10) & 0x1Fu) == 0x1Fu) return __uint_as_float(((h & 0x8000u) << 16) | 0x7F800000u | ((h & 0x3FFu) << 13));
-    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);  // finite values, subnormals included: exact
+    // finite values (subnormals included) convert exactly in hardware; Inf / NaN keep their bits as the reference
+    // widens them (the payload shifted up, no quieting): a select, not a branch
+    const float v = (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+    const float s = __uint_as_float(((h & 0x8000u) << 16) | 0x7F800000u | ((h & 0x3FFu) << 13));
+    return ((h >> 10) & 0x1Fu) == 0x1Fu ? s : v;
 }
+// f32 -> bf16 / f16, rounded to nearest even (tensor/cpu_dtype.go:73-123). f16: the hardware conversion rounds
+// finite values to nearest even, subnormal results and overflow to Inf included, as the reference does; a NaN is
+// sign | 0x7E00 | (mantissa >> 13) in the reference, chosen by a select.
 __device__ __forceinline__ uint32_t f32_to_h16(float f, int io) {
     uint32_t b = __float_as_uint(f);
     if (io == TRHIP_BF16) {
-        if ((b & 0x7FFFFFFFu) > 0x7F800000u) return ((b >> 16) | 0x0040u) & 0xFFFFu;
-        b += 0x7FFFu + ((b >> 16) & 1u);
-        return b >> 16;
+        const uint32_t nan = ((b >> 16) | 0x0040u) & 0xFFFFu;
+        const uint32_t r = (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+        return (b & 0x7FFFFFFFu) > 0x7F800000u ? nan : r;
     }
-    const uint32_t sign = (b >> 16) & 0x8000u;
-    const int us = (int)((b >> 23) & 0xFFu);
-    uint32_t ak = b & 0x7FFFFFu;
-    if (us == 0xFF) return ak ? (sign | 0x7E00u | (ak >> 13)) : (sign | 0x7C00u);
-    const int e = us - 127 + 15;
-    if (e >= 0x1F) return sign | 0x7C00u;
-    if (e <= 0) {
-        if (e < -10) return sign;
-        ak |= 0x800000u;
-        const uint32_t sh = (uint32_t)(14 - e);
-        uint32_t m = ak >> sh;
-        const uint32_t rest = ak & ((1u << sh) - 1u), half = 1u << (sh - 1);
-        if (rest > half || (rest == half && (m & 1u))) m++;
-        return sign | m;
-    }
-    uint32_t h = ((uint32_t)e << 10) | (ak >> 13);
-    const uint32_t rest = ak & 0x1FFFu;
-    if (rest > 0x1000u || (rest == 0x1000u && (h & 1u))) h++;
-    return sign | h;
+    const uint32_t hw = __builtin_bit_cast(uint16_t, (_Float16)f);
+    const uint32_t nan = ((b >> 16) & 0x8000u) | 0x7E00u | ((b & 0x7FFFFFu) >> 13);
+    return (b & 0x7FFFFFFFu) > 0x7F800000u ? nan : hw;
 }
 
 // Hide a value from the optimizer (no instruction is emitted). Used on a dword-wide nibble mask so the

@@ -102,6 +102,33 @@ def test_typed_fast_gemv_matches_fp32(backend, t, dt, N, K, acc):
 
 
 @pytest.mark.parametrize("t", [F16, BF16])
+@pytest.mark.parametrize("scale", [1e-6, 2e-5, 3e3, 1e4])
+@pytest.mark.parametrize("mode", [MODE_FAST, MODE_EXACT])
+def test_typed_rounding_ranges(backend, t, scale, mode):
+    """Outputs across the f16 subnormal range (scale 1e-6, 2e-5) and around its overflow edge (3e3, 1e4: row sums
+    past 65504 round to Inf): the bits of the oracle's rounding of the fp32 call on the widened activations, for the
+    fused batch-1 GEMV and the staged path (exact mode), both with c accumulated."""
+    N, K = 4096, 4096
+    raw = synth.quant_weights(Q4K, N, K, seed=31, outliers=0.01)
+    w = backend.FromQuantized(Q4K, raw, N, K)
+    rng = np.random.default_rng(int(scale * 1e6) % 1000 + 5)
+    xa, xw = _in(t, (rng.standard_normal(K) * scale).astype(np.float32))
+    ca, cw = _in(t, (rng.standard_normal(N) * scale).astype(np.float32))
+    got = _run(backend, w, 1, N, K, xa, t, ca, t, True, mode)
+    if mode == MODE_FAST:
+        y = _fast32(backend, w, N, K, xw, cw, True)
+    else:
+        y = O.quant_gemm(Q4K, 1, N, K, xw.reshape(1, K), raw, cw).reshape(-1)
+    want = O.round16(t, y)
+    _same(got, want, t)
+    if t == F16 and scale < 1e-4:
+        assert np.sum(np.abs(O.widen16(F16, want)) < 6.1e-5) > 100  # the subnormal range is exercised
+    if t == F16 and scale > 1e3:
+        assert np.isinf(O.widen16(F16, want)).any() or scale < 5e3
+    w.release()
+
+
+@pytest.mark.parametrize("t", [F16, BF16])
 def test_typed_special_values(backend, t):
     """NaN / Inf activations give the NaN / Inf outputs of the fp32 call through the rounding (the oracle's product
     in exact mode, the fp32 fast GEMV of the widened activations in fast mode); f16
