@@ -154,8 +154,9 @@ int trhip_gemm_q(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N,
  * gpu/backend_memory.go:41-52, 98-115): x is widened to fp32 exactly, the product is trhip_gemm_q's in fp32 (c
  * widened first when accumulating), and c is rounded to its type once, to nearest even (tensor/cpu_dtype.go:73-123:
  * NaN stays a quiet NaN, f16 overflows to Inf). Bit-identical to widening x, calling trhip_gemm_q and rounding its
- * result. The batch-1 fast GEMV with x and c of one 16-bit type reads and writes them directly (x 8-byte and c
- * 2-byte aligned); other cases go through fp32 copies in a workspace of the context. */
+ * result. With x and c of one 16-bit type (x 8-byte and c 2-byte aligned) the batch-1 GEMV (both modes) and the
+ * fast batched decode read and write them directly; other cases go through fp32 copies in a workspace of the
+ * context. */
 int trhip_gemm_q_typed(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const void *x, int xtype,
                        void *c, int ctype, int64_t M, int64_t K, int accumulate, int mode);
 

@@ -927,11 +927,21 @@ int trhip_gemm_q_typed(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int6
         if (ctype == TRHIP_F32) return zero_f32(ctx, static_cast<float *>(c), M * N);
         return fill_bytes(ctx, c, 0, (size_t)(M * N) * cb);
     }
-    // the decode GEMV with 16-bit x and c of one type: read and written directly by the K-across-lanes kernel
-    if (M == 1 && mode == TRHIP_MODE_FAST && xtype == ctype && reinterpret_cast<uintptr_t>(x) % 8 == 0 &&
-        reinterpret_cast<uintptr_t>(c) % 2 == 0) {
-        const int r = launch_gemv_fast_io(ctx, w, row0, N, x, c, accumulate != 0, xtype);
-        if (r != -1) return r;
+    // 16-bit x and c of one type, read and written directly: the exact decode GEMV; in fast mode the decode GEMV
+    // (K across lanes) and the batched decode kernel, where trhip_gemm_q takes them (q4_k from 5 rows, q4_0 from 2,
+    // up to 16)
+    if (mode == TRHIP_MODE_EXACT && M == 1 && xtype == ctype && reinterpret_cast<uintptr_t>(x) % 8 == 0 &&
+        reinterpret_cast<uintptr_t>(c) % 2 == 0)
+        return launch_gemv_exact_io(ctx, w, row0, N, x, c, accumulate != 0, xtype);
+    if (mode == TRHIP_MODE_FAST && xtype == ctype && reinterpret_cast<uintptr_t>(c) % 2 == 0) {
+        if (M == 1 && reinterpret_cast<uintptr_t>(x) % 8 == 0) {
+            const int r = launch_gemv_fast_io(ctx, w, row0, N, x, c, accumulate != 0, xtype);
+            if (r != -1) return r;
+        }
+        if (M <= 16 && ((w->dtype == TRHIP_Q4K && M > 4) || (w->dtype == TRHIP_Q4 && M > 1))) {
+            const int r = launch_rows16(ctx, w, row0, N, x, c, M, accumulate != 0, nullptr, xtype);
+            if (r != -1) return r;
+        }
     }
     // otherwise the reference's own sequence (gpu/backend_memory.go:41-52, 98-115): x widened to fp32, c widened when
     // accumulating, the fp32 operator, c rounded once

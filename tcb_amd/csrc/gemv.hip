@@ -16,6 +16,7 @@
 #include "trhip_internal.hpp"
 
 #include <cstdlib>
+#include <type_traits>
 
 namespace trhip {
 namespace {
@@ -25,11 +26,14 @@ namespace {
 // ahead of it: without it the compiler moves each load into its store's branch, and a wait follows each one.
 // A kernel issues the first batch, then its weight loads, then commits, so x and the first weights are in
 // flight together and the wait before the stores covers x only.
-template <int THREADS>
+// IO: fp32 x, or f16 / bf16 x read 8 bytes at a time and widened exactly on the way into LDS.
+template <int THREADS, int IO = TRHIP_F32>
 struct XStager {
     static constexpr int U = 8;
-    float4 v[U];
-    __device__ __forceinline__ void issue(const float4 *__restrict__ x4, int64_t n, int64_t i0) {
+    typedef typename std::conditional<IO == TRHIP_F32, float4, uint2>::type Raw;
+    Raw v[U];
+    __device__ __forceinline__ void issue(const void *__restrict__ xv, int64_t n, int64_t i0) {
+        const Raw *x4 = static_cast<const Raw *>(xv);
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int64_t i = i0 + (int64_t)u * THREADS + threadIdx.x;
@@ -39,19 +43,39 @@ struct XStager {
     __device__ __forceinline__ void commit(float4 *xs, int64_t n, int64_t i0) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            asm volatile("" : "+v"(v[u].x), "+v"(v[u].y), "+v"(v[u].z), "+v"(v[u].w));
+            float4 f;
+            if constexpr (IO == TRHIP_F32) {
+                asm volatile("" : "+v"(v[u].x), "+v"(v[u].y), "+v"(v[u].z), "+v"(v[u].w));
+                f = v[u];
+            } else {
+                asm volatile("" : "+v"(v[u].x), "+v"(v[u].y));
+                f = make_float4(h16_to_f32(v[u].x & 0xFFFFu, IO), h16_to_f32(v[u].x >> 16, IO),
+                                h16_to_f32(v[u].y & 0xFFFFu, IO), h16_to_f32(v[u].y >> 16, IO));
+            }
             const int64_t i = i0 + (int64_t)u * THREADS + threadIdx.x;
-            if (i < n) xs[i] = v[u];
+            if (i < n) xs[i] = f;
         }
     }
     // the batches after the first
-    __device__ __forceinline__ void rest(float4 *xs, const float4 *__restrict__ x4, int64_t n) {
+    __device__ __forceinline__ void rest(float4 *xs, const void *__restrict__ xv, int64_t n) {
         for (int64_t i0 = (int64_t)U * THREADS; i0 < n; i0 += (int64_t)U * THREADS) {
-            issue(x4, n, i0);
+            issue(xv, n, i0);
             commit(xs, n, i0);
         }
     }
 };
+
+// c[r] (+)= res: fp32, or 16-bit c widened, the fp32 sum, rounded once
+template <bool ACC, int IO>
+__device__ __forceinline__ void put_out(void *cv, int64_t r, float res) {
+    if constexpr (IO == TRHIP_F32) {
+        float *c = static_cast<float *>(cv);
+        c[r] = ACC ? c[r] + res : res;
+    } else {
+        uint16_t *c = static_cast<uint16_t *>(cv);
+        c[r] = (uint16_t)f32_to_h16(ACC ? h16_to_f32(c[r], IO) + res : res, IO);
+    }
+}
 
 __device__ __forceinline__ void fma4(float *acc, uint32_t codes, float s, float negm, float4 xv) {
     codes = opaque(codes);
@@ -208,9 +232,9 @@ struct Blk<kQ6K> {
     static constexpr int XSTEP = 64;
 };
 
-template <int DT, bool ACC, int THREADS>
-__global__ __launch_bounds__(THREADS) void gemv_exact_kernel(const Planes p, const float *__restrict__ x,
-                                                             float *__restrict__ c, int64_t N, int64_t row0, int64_t K) {
+template <int DT, bool ACC, int THREADS, int IO = TRHIP_F32>
+__global__ __launch_bounds__(THREADS) void gemv_exact_kernel(const Planes p, const void *__restrict__ x,
+                                                             void *__restrict__ c, int64_t N, int64_t row0, int64_t K) {
     extern __shared__ float4 xs[];  // K / 4 float4: the whole activation vector
     const int t = threadIdx.x & 3;
     const int64_t r = (int64_t)blockIdx.x * (THREADS / 4) + (threadIdx.x >> 2);
@@ -222,13 +246,13 @@ __global__ __launch_bounds__(THREADS) void gemv_exact_kernel(const Planes p, con
     B blk(p, row, t);
     typename B::Data ring[D];
     // x (cache-resident) and the first weight blocks (from HBM) in flight together, then x into LDS
-    XStager<THREADS> xst;
-    xst.issue(reinterpret_cast<const float4 *>(x), K / 4, 0);
+    XStager<THREADS, IO> xst;
+    xst.issue(x, K / 4, 0);
     __builtin_amdgcn_sched_barrier(0);  // x is requested first: the wait before its stores then skips the weights
 #pragma unroll
     for (int s = 0; s < D; s++) blk.load(ring[s], s < nb ? s : nb - 1);
     xst.commit(xs, K / 4, 0);
-    xst.rest(xs, reinterpret_cast<const float4 *>(x), K / 4);
+    xst.rest(xs, x, K / 4);
     __syncthreads();
 
     float acc[8];
@@ -247,10 +271,7 @@ __global__ __launch_bounds__(THREADS) void gemv_exact_kernel(const Planes p, con
         }
     }
     float res = sdot32_tree(acc);
-    if (live && t == 0) {
-        if (ACC) c[r] = c[r] + res;
-        else c[r] = res;
-    }
+    if (live && t == 0) put_out<ACC, IO>(c, r, res);
 }
 
 // ---------------------------------------------------------------- eight lanes per row
@@ -380,9 +401,9 @@ __device__ __forceinline__ float sdot32_tree8(const float *acc) {
     return (s[0] + s[2]) + (s[1] + s[3]);
 }
 
-template <int DT, bool ACC, int THREADS>
-__global__ __launch_bounds__(THREADS) void gemv_exact8_kernel(const Planes p, const float *__restrict__ x,
-                                                              float *__restrict__ c, int64_t N, int64_t row0, int64_t K) {
+template <int DT, bool ACC, int THREADS, int IO = TRHIP_F32>
+__global__ __launch_bounds__(THREADS) void gemv_exact8_kernel(const Planes p, const void *__restrict__ x,
+                                                              void *__restrict__ c, int64_t N, int64_t row0, int64_t K) {
     extern __shared__ float4 xs[];  // K / 4 float4: the whole activation vector
     const int u = threadIdx.x & 7;
     const int64_t r = (int64_t)blockIdx.x * (THREADS / 8) + (threadIdx.x >> 3);
@@ -393,13 +414,13 @@ __global__ __launch_bounds__(THREADS) void gemv_exact8_kernel(const Planes p, co
     constexpr int D = B::DEPTH;
     B blk(p, row, u);
     typename B::Data ring[D];
-    XStager<THREADS> xst;
-    xst.issue(reinterpret_cast<const float4 *>(x), K / 4, 0);
+    XStager<THREADS, IO> xst;
+    xst.issue(x, K / 4, 0);
     __builtin_amdgcn_sched_barrier(0);  // x is requested first: the wait before its stores then skips the weights
 #pragma unroll
     for (int s = 0; s < D; s++) blk.load(ring[s], s < nb ? s : nb - 1);
     xst.commit(xs, K / 4, 0);
-    xst.rest(xs, reinterpret_cast<const float4 *>(x), K / 4);
+    xst.rest(xs, x, K / 4);
     __syncthreads();
 
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -414,30 +435,27 @@ __global__ __launch_bounds__(THREADS) void gemv_exact8_kernel(const Planes p, co
         }
     }
     const float res = sdot32_tree8(acc);
-    if (live && u == 0) {
-        if (ACC) c[r] = c[r] + res;
-        else c[r] = res;
-    }
+    if (live && u == 0) put_out<ACC, IO>(c, r, res);
 }
 
 template <int DT, int THREADS>
-void launch_exact8_t(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
-                     bool acc, size_t lds) {
+void launch_exact8_t(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const void *x, void *c,
+                     bool acc, size_t lds, int io) {
     dim3 grid((unsigned)((N + THREADS / 8 - 1) / (THREADS / 8))), block(THREADS);
-    if (acc)
-        hipLaunchKernelGGL((gemv_exact8_kernel<DT, true, THREADS>), grid, block, lds, ctx->stream, w->planes(), x, c, N, row0, w->K);
-    else
-        hipLaunchKernelGGL((gemv_exact8_kernel<DT, false, THREADS>), grid, block, lds, ctx->stream, w->planes(), x, c, N, row0, w->K);
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, block, lds, ctx->stream, w->planes(), x, c, N, row0, w->K); };
+    if (io == TRHIP_F16) acc ? go(gemv_exact8_kernel<DT, true, THREADS, TRHIP_F16>) : go(gemv_exact8_kernel<DT, false, THREADS, TRHIP_F16>);
+    else if (io == TRHIP_BF16) acc ? go(gemv_exact8_kernel<DT, true, THREADS, TRHIP_BF16>) : go(gemv_exact8_kernel<DT, false, THREADS, TRHIP_BF16>);
+    else acc ? go(gemv_exact8_kernel<DT, true, THREADS>) : go(gemv_exact8_kernel<DT, false, THREADS>);
 }
 
 template <int DT, int THREADS>
-void launch_exact_t(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
-                    bool acc, size_t lds) {
+void launch_exact_t(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const void *x, void *c,
+                    bool acc, size_t lds, int io) {
     dim3 grid((unsigned)((N + THREADS / 4 - 1) / (THREADS / 4))), block(THREADS);
-    if (acc)
-        hipLaunchKernelGGL((gemv_exact_kernel<DT, true, THREADS>), grid, block, lds, ctx->stream, w->planes(), x, c, N, row0, w->K);
-    else
-        hipLaunchKernelGGL((gemv_exact_kernel<DT, false, THREADS>), grid, block, lds, ctx->stream, w->planes(), x, c, N, row0, w->K);
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, block, lds, ctx->stream, w->planes(), x, c, N, row0, w->K); };
+    if (io == TRHIP_F16) acc ? go(gemv_exact_kernel<DT, true, THREADS, TRHIP_F16>) : go(gemv_exact_kernel<DT, false, THREADS, TRHIP_F16>);
+    else if (io == TRHIP_BF16) acc ? go(gemv_exact_kernel<DT, true, THREADS, TRHIP_BF16>) : go(gemv_exact_kernel<DT, false, THREADS, TRHIP_BF16>);
+    else acc ? go(gemv_exact_kernel<DT, true, THREADS>) : go(gemv_exact_kernel<DT, false, THREADS>);
 }
 
 // Rows per workgroup: the largest of 64, 32, 16 that still gives >= 200 workgroups (64 measured fastest on
@@ -450,8 +468,8 @@ int gemv_rows_per_wg(const trhip_ctx *ctx, int64_t N) {
 }
 
 template <int DT>
-int launch_exact(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
-                 bool acc) {
+int launch_exact(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const void *x, void *c,
+                 bool acc, int io = TRHIP_F32) {
     size_t lds = (size_t)w->K * sizeof(float);
     if (lds > 160 * 1024) return fail(ctx, TRHIP_ERR_UNSUPPORTED, "gemv: K too large for the LDS copy of x");
     // lanes per row: 8 measured faster for q4_k (14336x4096 cold: 15.7 vs 18.0 us; 1024x4096: 12.5 vs 15.9),
@@ -464,15 +482,15 @@ int launch_exact(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N,
         // (cold, us, 128 -> 64 threads, bit-identical: q4_k 1024x4096 11.0 -> 10.66, 2048x4096 11.1 -> 10.8,
         // 1024x14336 33.6 -> 32.1; q8_0 / q4_0 1024x4096 18.3 / 18.1 -> 17.9 / 17.2); q4_k keeps 16 rows per workgroup
         // on large grids too (14336x4096 13.86 -> 13.7, 28672x4096 22.8 -> 22.4; q8_0 / q4_0 lose 1%)
-        if (N >= 32 * 200 && DT != kQ4K) launch_exact8_t<DT, 256>(ctx, w, row0, N, x, c, acc, lds);
-        else if (N >= 16 * 200) launch_exact8_t<DT, 128>(ctx, w, row0, N, x, c, acc, lds);
-        else launch_exact8_t<DT, 64>(ctx, w, row0, N, x, c, acc, lds);
+        if (N >= 32 * 200 && DT != kQ4K) launch_exact8_t<DT, 256>(ctx, w, row0, N, x, c, acc, lds, io);
+        else if (N >= 16 * 200) launch_exact8_t<DT, 128>(ctx, w, row0, N, x, c, acc, lds, io);
+        else launch_exact8_t<DT, 64>(ctx, w, row0, N, x, c, acc, lds, io);
         return launch_check(ctx, "gemv_exact8");
     }
     switch (gemv_rows_per_wg(ctx, N)) {
-    case 64: launch_exact_t<DT, 256>(ctx, w, row0, N, x, c, acc, lds); break;
-    case 32: launch_exact_t<DT, 128>(ctx, w, row0, N, x, c, acc, lds); break;
-    default: launch_exact_t<DT, 64>(ctx, w, row0, N, x, c, acc, lds); break;
+    case 64: launch_exact_t<DT, 256>(ctx, w, row0, N, x, c, acc, lds, io); break;
+    case 32: launch_exact_t<DT, 128>(ctx, w, row0, N, x, c, acc, lds, io); break;
+    default: launch_exact_t<DT, 64>(ctx, w, row0, N, x, c, acc, lds, io); break;
     }
     return launch_check(ctx, "gemv_exact");
 }
@@ -491,6 +509,20 @@ int launch_gemv(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, 
     case kQ4: return launch_exact<kQ4>(ctx, w, row0, N, x, c, acc);
     case kQ4K: return launch_exact<kQ4K>(ctx, w, row0, N, x, c, acc);
     case kQ6K: return launch_exact<kQ6K>(ctx, w, row0, N, x, c, acc);
+    }
+    return fail(ctx, TRHIP_ERR_INVALID, "gemv: bad dtype");
+}
+
+// The exact GEMV with f16 / bf16 x (8-byte aligned) and c of that type: x widened on its way into LDS, c widened,
+// the row's result added, rounded once (the bits of the fp32 call on the widened values, rounded).
+int launch_gemv_exact_io(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const void *x, void *c,
+                         bool acc, int io) {
+    if (N == 0) return TRHIP_OK;
+    switch (w->dtype) {
+    case kQ8: return launch_exact<kQ8>(ctx, w, row0, N, x, c, acc, io);
+    case kQ4: return launch_exact<kQ4>(ctx, w, row0, N, x, c, acc, io);
+    case kQ4K: return launch_exact<kQ4K>(ctx, w, row0, N, x, c, acc, io);
+    case kQ6K: return launch_exact<kQ6K>(ctx, w, row0, N, x, c, acc, io);
     }
     return fail(ctx, TRHIP_ERR_INVALID, "gemv: bad dtype");
 }

@@ -103,19 +103,27 @@ __device__ __forceinline__ v8h r16_codes(const R16W &r, const R16K &k, int s, ui
 // plane, msum operands, exponents, NaN / Inf flags), laid out as the MFMA reads them (step s, lane l at 64 s + l).
 // q4_0 (DT = kQ4): step s is 32-element block s of the 256, and lane group gq holds its elements 4 gq + (0, 2, 1, 3)
 // (the low nibbles of code bytes 4 gq .. 4 gq + 3) and 16 + 4 gq + (0, 2, 1, 3) (their high nibbles); no msum.
-template <int DT>
-__global__ __launch_bounds__(R16_THREADS) void halves16_kernel(const float *__restrict__ x, int64_t M, int64_t K,
+// IO: fp32 x, or f16 / bf16 x widened exactly on load (the record is then that of the widened x).
+template <int DT, int IO = TRHIP_F32>
+__global__ __launch_bounds__(R16_THREADS) void halves16_kernel(const void *__restrict__ xv, int64_t M, int64_t K,
                                                                uint8_t *__restrict__ rec) {
     const int b = blockIdx.x, tid = threadIdx.x;
     uint8_t *st = rec + (int64_t)b * R16_XREC;
     // thread (pm, pu) holds elements 16 pu .. 16 pu + 15 of row pm of the block
     const int pm = tid >> 4, pu = tid & 15;
     const bool prow = pm < M;
-    const float4 *xp = reinterpret_cast<const float4 *>(x + (prow ? pm : 0) * K + 256 * (int64_t)b + 16 * pu);
+    const int64_t e0 = (prow ? pm : 0) * K + 256 * (int64_t)b + 16 * pu;
     float v[16];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const float4 q = xp[i];
+        float4 q;
+        if constexpr (IO == TRHIP_F32) {
+            q = reinterpret_cast<const float4 *>(static_cast<const float *>(xv) + e0)[i];
+        } else {
+            const uint2 hh = reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(xv) + e0)[i];
+            q = make_float4(h16_to_f32(hh.x & 0xFFFFu, IO), h16_to_f32(hh.x >> 16, IO), h16_to_f32(hh.y & 0xFFFFu, IO),
+                            h16_to_f32(hh.y >> 16, IO));
+        }
         v[4 * i] = prow ? q.x : 0.0f;
         v[4 * i + 1] = prow ? q.y : 0.0f;
         v[4 * i + 2] = prow ? q.z : 0.0f;
@@ -206,13 +214,29 @@ struct R16Stage {  // one block in LDS: the activation record, the R rows' heade
 // eight fp16 scales, its 128 qs bytes their codes, so the staging is the same)
 // (two waves per SIMD, which the LDS allows anyway: with the register budget of that occupancy the products stay in
 // VGPRs rather than being copied out of the accumulator registers)
-template <int DT, int TPW, bool ACC, bool SWI>
+// IO: fp32 x and c, or f16 / bf16 x and c (x widened exactly, c widened, the fp32 result added, rounded once);
+// not with SWI, whose gated output is fp32
+template <int DT, int TPW, bool ACC, bool SWI, int IO = TRHIP_F32>
 __global__ __launch_bounds__(R16_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void rows16_gemm(const Planes p, int64_t nrows, int64_t N, int64_t row0,
-                                                           int64_t M, int64_t K, const float *__restrict__ x,
+                                                           int64_t M, int64_t K, const void *__restrict__ xv,
                                                            const uint8_t *__restrict__ rec, int64_t RT, int S, int bps,
-                                                           float *__restrict__ c, float *__restrict__ part,
+                                                           void *__restrict__ cv, float *__restrict__ part,
                                                            uint32_t *__restrict__ arrivals) {
     static_assert(DT == kQ4K || (DT == kQ4 && !SWI), "q4_k, or q4_0 without the gate");
+    static_assert(IO == TRHIP_F32 || !SWI, "the gated output is fp32");
+    float *c = static_cast<float *>(cv);  // (IO == TRHIP_F32)
+    auto xat = [&](int64_t i) -> float {  // element i of x, widened
+        if constexpr (IO == TRHIP_F32) return static_cast<const float *>(xv)[i];
+        else return h16_to_f32(static_cast<const uint16_t *>(xv)[i], IO);
+    };
+    auto cput = [&](int64_t i, float v) {  // c[i] (+)= v, rounded once when 16-bit
+        if constexpr (IO == TRHIP_F32) {
+            c[i] = ACC ? c[i] + v : v;
+        } else {
+            uint16_t *c16 = static_cast<uint16_t *>(cv);
+            c16[i] = (uint16_t)f32_to_h16(ACC ? h16_to_f32(c16[i], IO) + v : v, IO);
+        }
+    };
     using T = R16Stage<TPW>;
     constexpr int R = T::R, H = R / 2;
     // three stages as separate arrays: the compiler then sees that the reads of one stage do not alias the DMA
@@ -426,8 +450,7 @@ __global__ __launch_bounds__(R16_THREADS) __attribute__((amdgpu_waves_per_eu(2, 
             const int m = 4 * g + r;
             if (m >= M || rowbad[m]) continue;
             if (direct) {
-                float *o = c + m * N + rt * R + nl;
-                *o = ACC ? *o + acc[tt][r] : acc[tt][r];
+                cput(m * N + rt * R + nl, acc[tt][r]);
             } else {
                 put(m * R + nl, acc[tt][r]);
             }
@@ -447,9 +470,8 @@ __global__ __launch_bounds__(R16_THREADS) __attribute__((amdgpu_waves_per_eu(2, 
             float a = 0.0f;
             if (act) {
                 const int64_t row = row0 + out_row(nl);
-                const float *xr = x + m * K;
                 for (int64_t k = 256 * (int64_t)c0; k < 256 * (int64_t)c1; k += 32)
-                    a = fmaf(xr[k + l32], deq_at<DT>(p, row, k + l32), a);
+                    a = fmaf(xat(m * K + k + l32), deq_at<DT>(p, row, k + l32), a);
             }
             float v = a + __shfl_xor(a, 8);
             v = v + __shfl_xor(v, 16);
@@ -458,8 +480,7 @@ __global__ __launch_bounds__(R16_THREADS) __attribute__((amdgpu_waves_per_eu(2, 
             v = v + __shfl_xor(v, 1);
             if (act && l32 == 0) {
                 if (direct) {
-                    float *o = c + m * N + rt * R + nl;
-                    *o = ACC ? *o + v : v;
+                    cput(m * N + rt * R + nl, v);
                 } else {
                     put(m * R + nl, v);
                 }
@@ -507,8 +528,7 @@ __global__ __launch_bounds__(R16_THREADS) __attribute__((amdgpu_waves_per_eu(2, 
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 if (rt * R + nl + e >= N) break;
-                float *o = c + m * N + rt * R + nl + e;
-                *o = ACC ? *o + sv[e] : sv[e];
+                cput(m * N + rt * R + nl + e, sv[e]);
             }
         }
     } else {
@@ -553,28 +573,29 @@ __global__ __launch_bounds__(R16_THREADS) __attribute__((amdgpu_waves_per_eu(2, 
 
 template <int DT, int TPW>
 int run_rows16(trhip_ctx *ctx, const Planes &pl, int64_t nrows, int64_t N, int64_t row0, int64_t M, int64_t K,
-               const float *x, const uint8_t *rec, int64_t RT, int S, int bps, float *c, float *part, bool acc,
-               bool swi) {
+               const void *x, const uint8_t *rec, int64_t RT, int S, int bps, void *c, float *part, bool acc,
+               bool swi, int io) {
     const dim3 grid((unsigned)(RT * S)), block(R16_THREADS);
-    if (swi)
-        hipLaunchKernelGGL((rows16_gemm<kQ4K, TPW, false, true>), grid, block, 0, ctx->stream, pl, nrows, N, row0, M, K, x,
-                           rec, RT, S, bps, c, part, ctx->arrivals);
-    else if (acc)
-        hipLaunchKernelGGL((rows16_gemm<DT, TPW, true, false>), grid, block, 0, ctx->stream, pl, nrows, N, row0, M, K, x,
-                           rec, RT, S, bps, c, part, ctx->arrivals);
-    else
-        hipLaunchKernelGGL((rows16_gemm<DT, TPW, false, false>), grid, block, 0, ctx->stream, pl, nrows, N, row0, M, K, x,
-                           rec, RT, S, bps, c, part, ctx->arrivals);
-    return launch_check(ctx, "rows16_gemm");
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, block, 0, ctx->stream, pl, nrows, N, row0, M, K, x, rec, RT, S, bps, c, part,
+                           ctx->arrivals);
+        return launch_check(ctx, "rows16_gemm");
+    };
+    if (swi) return go(rows16_gemm<kQ4K, TPW, false, true>);
+    if (io == TRHIP_F16) return acc ? go(rows16_gemm<DT, TPW, true, false, TRHIP_F16>) : go(rows16_gemm<DT, TPW, false, false, TRHIP_F16>);
+    if (io == TRHIP_BF16) return acc ? go(rows16_gemm<DT, TPW, true, false, TRHIP_BF16>) : go(rows16_gemm<DT, TPW, false, false, TRHIP_BF16>);
+    return acc ? go(rows16_gemm<DT, TPW, true, false>) : go(rows16_gemm<DT, TPW, false, false>);
 }
 
 }  // namespace
 
-int launch_rows16(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
-                  int64_t M, bool acc, float *swi) {
+int launch_rows16(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const void *x, void *c,
+                  int64_t M, bool acc, float *swi, int io) {
     const int dt = w->dtype;
     if ((dt != kQ4K && dt != kQ4) || M < 1 || M > 16 || w->K <= 0 || w->K % 256 != 0) return -1;
     if (dt == kQ4 && swi) return -1;  // the gate is fused for q4_k only
+    if (swi && io != TRHIP_F32) return -1;
+    const size_t xel = io == TRHIP_F32 ? sizeof(float) : sizeof(uint16_t);
     const int64_t K = w->K, nb = K / 256;
     const bool fused = swi != nullptr;
     if (fused && (N % 2 != 0 || acc)) return -1;
@@ -606,35 +627,37 @@ int launch_rows16(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N
     if (S > 1 && RT > trhip_ctx::kArrivalSlots) return -1;
     // the weight DMAs address a plane with 32-bit offsets
     if (w->N * nb * 128 > (int64_t)UINT32_MAX) return -1;
-    const bool copy_x = reinterpret_cast<uintptr_t>(x) % 16 != 0;
+    // the record kernel reads x 16 bytes (fp32) or 8 bytes (16-bit) at a time
+    const bool copy_x = reinterpret_cast<uintptr_t>(x) % (io == TRHIP_F32 ? 16 : 8) != 0;
     auto al = [](size_t v) { return (v + 255) / 256 * 256; };
-    const size_t o_x = 0, o_r = al(copy_x ? (size_t)(M * K) * sizeof(float) : 0);
+    const size_t o_x = 0, o_r = al(copy_x ? (size_t)(M * K) * xel : 0);
     const size_t o_p = al(o_r + (size_t)nb * R16_XREC);
     const bool need_part = fused || S > 1;
     const size_t total = o_p + (need_part ? (size_t)(RT * S * 16 * R) * sizeof(float) : 0);
     int st = TRHIP_OK;
     uint8_t *ws = static_cast<uint8_t *>(workspace(ctx, total, &st));
     if (!ws) return st;
-    const float *xa = x;
+    const void *xa = x;
     if (copy_x) {
-        hipError_t e = hipMemcpyAsync(ws + o_x, x, (size_t)(M * K) * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream);
+        hipError_t e = hipMemcpyAsync(ws + o_x, x, (size_t)(M * K) * xel, hipMemcpyDeviceToDevice, ctx->stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "rows16: align x");
-        xa = reinterpret_cast<const float *>(ws + o_x);
+        xa = ws + o_x;
     }
     uint8_t *rec = ws + o_r;
-    if (dt == kQ4)
-        hipLaunchKernelGGL(halves16_kernel<kQ4>, dim3((unsigned)nb), dim3(R16_THREADS), 0, ctx->stream, xa, M, K, rec);
-    else
-        hipLaunchKernelGGL(halves16_kernel<kQ4K>, dim3((unsigned)nb), dim3(R16_THREADS), 0, ctx->stream, xa, M, K, rec);
+    const dim3 rg((unsigned)nb), rb(R16_THREADS);
+    auto rec_go = [&](auto kern) { hipLaunchKernelGGL(kern, rg, rb, 0, ctx->stream, xa, M, K, rec); };
+    if (io == TRHIP_F16) dt == kQ4 ? rec_go(halves16_kernel<kQ4, TRHIP_F16>) : rec_go(halves16_kernel<kQ4K, TRHIP_F16>);
+    else if (io == TRHIP_BF16) dt == kQ4 ? rec_go(halves16_kernel<kQ4, TRHIP_BF16>) : rec_go(halves16_kernel<kQ4K, TRHIP_BF16>);
+    else dt == kQ4 ? rec_go(halves16_kernel<kQ4>) : rec_go(halves16_kernel<kQ4K>);
     if ((st = launch_check(ctx, "halves16")) != TRHIP_OK) return st;
     float *part = need_part ? reinterpret_cast<float *>(ws + o_p) : nullptr;
-    float *dst = fused ? swi : c;
+    void *dst = fused ? static_cast<void *>(swi) : c;
     const Planes pl = w->planes();
     if (dt == kQ4)
-        return tpw == 2 ? run_rows16<kQ4, 2>(ctx, pl, w->N, N, row0, M, K, xa, rec, RT, S, bps, dst, part, acc, false)
-                        : run_rows16<kQ4, 1>(ctx, pl, w->N, N, row0, M, K, xa, rec, RT, S, bps, dst, part, acc, false);
-    if (tpw == 2) return run_rows16<kQ4K, 2>(ctx, pl, w->N, N, row0, M, K, xa, rec, RT, S, bps, dst, part, acc, fused);
-    return run_rows16<kQ4K, 1>(ctx, pl, w->N, N, row0, M, K, xa, rec, RT, S, bps, dst, part, acc, fused);
+        return tpw == 2 ? run_rows16<kQ4, 2>(ctx, pl, w->N, N, row0, M, K, xa, rec, RT, S, bps, dst, part, acc, false, io)
+                        : run_rows16<kQ4, 1>(ctx, pl, w->N, N, row0, M, K, xa, rec, RT, S, bps, dst, part, acc, false, io);
+    if (tpw == 2) return run_rows16<kQ4K, 2>(ctx, pl, w->N, N, row0, M, K, xa, rec, RT, S, bps, dst, part, acc, fused, io);
+    return run_rows16<kQ4K, 1>(ctx, pl, w->N, N, row0, M, K, xa, rec, RT, S, bps, dst, part, acc, fused, io);
 }
 
 }  // namespace trhip

@@ -401,6 +401,9 @@ int launch_round16(trhip_ctx *ctx, const float *src, uint16_t *dst, int64_t n, i
 // store's shape does not take that kernel.
 int launch_gemv_fast_io(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const void *x, void *c,
                         bool acc, int io);
+// The exact GEMV with 16-bit x (8-byte aligned) and c of one type (gemv.hip).
+int launch_gemv_exact_io(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const void *x, void *c,
+                         bool acc, int io);
 void *workspace3(trhip_ctx *ctx, size_t bytes, int *status);
 
 // The prefill kernels' inner loop alone on their real grid (prefill.hip): kind 0 q4_k exact, 1 q4_k fast, 2 q6_k.
@@ -408,8 +411,9 @@ int launch_prefill_probe(trhip_ctx *ctx, int kind, int64_t M, int64_t N, int64_t
 int launch_mfma_probe(trhip_ctx *ctx, int valu_per_mfma, int waves_per_simd, int64_t iters);
 // Fast-mode q4_k product for 1 <= M <= 16 activation rows in one launch (rows16.hip); swi as in
 // launch_gemm_rows_fast. Returns -1 (nothing launched) where it does not apply.
-int launch_rows16(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,
-                      int64_t M, bool acc, float *swi = nullptr);
+// io: TRHIP_F32, or f16 / bf16 x and c (read and written directly; not with swi).
+int launch_rows16(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const void *x, void *c,
+                      int64_t M, bool acc, float *swi = nullptr, int io = TRHIP_F32);
 // q4_0 and q6_k act-quant on int8 matrix cores (actq4.hip, actq6.hip): whether each takes the shape, and the kernel.
 bool actq4_mfma_applies(int64_t M, int64_t N, int64_t row0, int64_t K);
 int launch_actq4_mfma(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const float *x, float *c,

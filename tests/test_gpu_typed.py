@@ -188,3 +188,80 @@ def test_typed_unaligned_and_refusals(backend):
     for b in (xb, cb):
         b.free()
     w.release()
+
+
+@pytest.mark.parametrize("t", [F16, BF16])
+@pytest.mark.parametrize("M,mode", [(1, MODE_FAST), (1, MODE_EXACT), (6, MODE_FAST)])
+def test_typed_row_slice(backend, t, M, mode):
+    """A row slice of the store (row0 = 7, N = 2000 of 2100 rows): the bits of the same call on the fp32 entry
+    point over the widened activations, rounded once."""
+    R, N, K, row0 = 2100, 2000, 4096, 7
+    raw = synth.quant_weights(Q4K, R, K, seed=77, outliers=0.01)
+    w = backend.FromQuantized(Q4K, raw, R, K)
+    rng = np.random.default_rng(M + 3)
+    xa, xw = _in(t, rng.standard_normal(M * K).astype(np.float32))
+    ca, cw = _in(t, rng.standard_normal(M * N).astype(np.float32))
+    xb, cb = backend.ctx.to_device(xa), backend.ctx.to_device(ca)
+    backend.GemmTyped(M, N, K, xb, t, w, cb, t, row0=row0, accumulate=True, mode=mode)
+    got = cb.download(np.uint16, M * N)
+    xb.free()
+    cb.free()
+    xb, cb = backend.ctx.to_device(xw), backend.ctx.to_device(cw)
+    backend.Gemm(M, N, K, xb, w, cb, row0=row0, mode=mode)
+    want = O.round16(t, cb.download(np.float32, M * N))
+    xb.free()
+    cb.free()
+    _same(got, want, t)
+    w.release()
+
+
+def _fast32m(backend, w, M, N, K, xw, cw, acc, row0=0):
+    """The fp32 fast call of M rows on the widened activations (on the widened c when accumulating)."""
+    xb, cb = backend.ctx.to_device(xw), backend.ctx.to_device(cw)
+    (backend.Gemm if acc else backend.GemmSet)(M, N, K, xb, w, cb, row0=row0, mode=MODE_FAST)
+    y = cb.download(np.float32, M * N)
+    xb.free()
+    cb.free()
+    return y
+
+
+@pytest.mark.parametrize("t", [F16, BF16])
+@pytest.mark.parametrize("dt,M,N,K", [(Q4K, 16, 14336, 4096), (Q4K, 5, 1000, 4096), (Q4K, 9, 4096, 14336),
+                                      (Q4, 2, 4096, 4096), (Q4, 8, 300, 2048), (Q4K, 16, 28672, 1024)])
+@pytest.mark.parametrize("acc", [False, True])
+def test_typed_batched_fast_bits(backend, t, dt, M, N, K, acc):
+    """Batched decode (q4_k 5..16 rows, q4_0 2..16) with x and c of one 16-bit type, read and written by the batched
+    kernels themselves (one K slice, several slices summed by the last workgroup, 128-row tiles): the bits of the
+    fp32 fast call on the widened activations and c, rounded once."""
+    raw = synth.quant_weights(dt, N, K, seed=N + M, outliers=0.01 if dt == Q4K else 0.0)
+    w = backend.FromQuantized(dt, raw, N, K)
+    rng = np.random.default_rng(M * 3 + N)
+    xa, xw = _in(t, rng.standard_normal(M * K).astype(np.float32))
+    ca, cw = _in(t, (rng.standard_normal(M * N) * 3).astype(np.float32))
+    got = _run(backend, w, M, N, K, xa, t, ca, t, acc, MODE_FAST)
+    _same(got, O.round16(t, _fast32m(backend, w, M, N, K, xw, cw, acc)), t)
+    w.release()
+
+
+@pytest.mark.parametrize("t", [F16, BF16])
+def test_typed_batched_nan_rows_and_alignment(backend, t):
+    """NaN / Inf activation rows (the exact float fallback reads the 16-bit x), a row slice, and an x that is only
+    2-byte aligned (copied first): the bits of the fp32 fast call on the widened values, rounded once."""
+    R, N, K, M, row0 = 1200, 1000, 4096, 7, 100
+    raw = synth.quant_weights(Q4K, R, K, seed=5, outliers=0.01)
+    w = backend.FromQuantized(Q4K, raw, R, K)
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x[2, 100] = np.nan
+    x[5, 4000] = np.inf
+    xa, xw = _in(t, x.reshape(-1))
+    ca, cw = _in(t, rng.standard_normal(M * N).astype(np.float32))
+    xb = backend.ctx.alloc(M * K * 2 + 16)
+    xb.upload(xa, byte_offset=2)
+    cb = backend.ctx.to_device(ca)
+    backend.GemmTyped(M, N, K, (xb, 2), t, w, cb, t, row0=row0, accumulate=True, mode=MODE_FAST)
+    got = cb.download(np.uint16, M * N)
+    xb.free()
+    cb.free()
+    _same(got, O.round16(t, _fast32m(backend, w, M, N, K, xw, cw, True, row0=row0)), t)
+    w.release()
