@@ -583,8 +583,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const void
             a = fmaf(n1, sxh, a);
             if (!fin) {  // Inf or NaN in this lane's x: dequantized values times x in float
                 a = 0.0f;
-#pragma unroll
-                for (int k = 0; k < 8; k++) {
+                auto part = [&](int k) {
                     const float4 xl = x4(k), xh = x4(8 + k);
                     const uint32_t lo = qw[k] & 0x0F0F0F0Fu, hi = (qw[k] >> 4) & 0x0F0F0F0Fu;
                     const float xlv[4] = {xl.x, xl.y, xl.z, xl.w}, xhv[4] = {xh.x, xh.y, xh.z, xh.w};
@@ -593,6 +592,13 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kl(const Planes p, const void
                         a = fmaf(fmaf(s0, ubyte_f(lo, t), n0), xlv[t], a);
                         a = fmaf(fmaf(s1, ubyte_f(hi, t), n1), xhv[t], a);
                     }
+                };
+                if constexpr (IO == TRHIP_F32) {
+#pragma unroll
+                    for (int k = 0; k < 8; k++) part(k);
+                } else {  // rolled: widening x here would otherwise grow every row slot's code past what unrolls
+#pragma unroll 1
+                    for (int k = 0; k < 8; k++) part(k);
                 }
             }
             } else {
