@@ -10,7 +10,10 @@
 // (byte j holds elements j and j + 16, tensor/quant.go:149-155); lane l of the A operand the same elements of
 // activation row l % 32. The result's lane l holds rows 8 j + 4 (l / 32) + r (j, r < 4) of column l % 32 (the
 // layout the 32x32 int8 products of the other matrix-core kernels use), so each lane owns sixteen outputs of one
-// weight row; the epilogue is four VALU per output and block, which is what bounds this kernel.
+// weight row. The scale products t of a block's 64 x 32 outputs come from the matrix cores too (a two-block
+// 32x32x1 fp32 product of the d8 column and the d_w row, in the same layout), which leaves the VALU three
+// instructions per output and block (convert, multiply, add: the reference's rounding steps, unfused); the VALU is
+// what bounds this kernel, so the products of block b + 1 are issued before block b is folded in.
 //
 // Tiling: a workgroup is 4 waves over 128 weight rows (32 per wave) and 64 activation rows (two 32-row tiles).
 // Eight blocks (256 elements) form one LDS stage: the activation and weight codes in swizzled 16-byte pieces, the
@@ -125,39 +128,53 @@ __global__ __launch_bounds__(Q4A_THREADS) __attribute__((amdgpu_waves_per_eu(2, 
 #pragma unroll
         for (int v = 0; v < 16; v++) acc[t][v] = 0.0f;
 
+    // One block's products: C[t] = the int8 sums of activation tile t (32x32x32 i8), T = t = fl(d_w d8) for both
+    // tiles as the two-block 32x32x1 fp32 product (block t = tile t: lane l gives A = d8 of activation row l of the
+    // 64, B = d_w of weight row l % 32; D = a b + 0, one rounding, registers 16 t .. +15 in the int8 product's
+    // layout).
+    auto products = [&](const uint8_t *sb, int bb, v16i (&C)[Q4A_MT], v32f &T) {
+        const uint4 raw = *reinterpret_cast<const uint4 *>(sb + L::O_W + 16 * q4a_w_slot(wrow, bb));
+        const uint32_t rw4[4] = {raw.x, raw.y, raw.z, raw.w};
+        v4i B;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {  // q4 - 8 as bytes: q + 120 never carries out of a byte, xor 128
+            const uint32_t nib = h ? ((rw4[e] >> 4) & 0x0F0F0F0Fu) : (rw4[e] & 0x0F0F0F0Fu);
+            B[e] = (int)((nib + 0x78787878u) ^ 0x80808080u);
+        }
+        const float d8 = reinterpret_cast<const float *>(sb + L::O_D8)[Q4A_TM * bb + lane];
+        const float dw = f16_to_f32(reinterpret_cast<const uint16_t *>(sb + L::O_DW)[Q4A_BPS * wrow + bb]);
+        T = __builtin_amdgcn_mfma_f32_32x32x1f32(d8, dw, (v32f){0.0f}, 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < Q4A_MT; t++) {
+            const v4i A = *reinterpret_cast<const v4i *>(sb + 16 * q4a_act_slot(32 * t + nl, 2 * bb + h));
+            C[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, (v16i){0}, 0, 0, 0);
+        }
+    };
+
     stage(0, 0);
     for (int s = 0; s < ns; s++) {
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
         // stage s has landed (this wave's copies, then everyone's at the barrier); nobody reads the other
         if (s + 1 < ns) stage(s + 1, (s + 1) & 1);
         const uint8_t *sb = lds + (s & 1) * L::STAGE;
-        const float *d8s = reinterpret_cast<const float *>(sb + L::O_D8);
-        const uint16_t *dws = reinterpret_cast<const uint16_t *>(sb + L::O_DW);
-#pragma unroll 2
+        // software-pipelined over the stage's blocks: block bb + 1's products are in flight on the matrix cores
+        // while the VALU folds block bb's into the sums
+        v16i C[Q4A_MT];
+        v32f T;
+        products(sb, 0, C, T);
+#pragma unroll
         for (int bb = 0; bb < Q4A_BPS; bb++) {
-            const uint4 raw = *reinterpret_cast<const uint4 *>(sb + L::O_W + 16 * q4a_w_slot(wrow, bb));
-            const uint32_t rw4[4] = {raw.x, raw.y, raw.z, raw.w};
-            v4i B;
+            v16i Cn[Q4A_MT];
+            v32f Tn;
+            if (bb + 1 < Q4A_BPS) products(sb, bb + 1, Cn, Tn);
 #pragma unroll
-            for (int e = 0; e < 4; e++) {  // q4 - 8 as bytes: q + 120 never carries out of a byte, xor 128
-                const uint32_t nib = h ? ((rw4[e] >> 4) & 0x0F0F0F0Fu) : (rw4[e] & 0x0F0F0F0Fu);
-                B[e] = (int)((nib + 0x78787878u) ^ 0x80808080u);
-            }
-            const float dw = f16_to_f32(dws[Q4A_BPS * wrow + bb]);
+            for (int t = 0; t < Q4A_MT; t++)
 #pragma unroll
-            for (int t = 0; t < Q4A_MT; t++) {
-                const v4i A = *reinterpret_cast<const v4i *>(sb + 16 * q4a_act_slot(32 * t + nl, 2 * bb + h));
-                const v16i C = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, (v16i){0}, 0, 0, 0);
+                for (int v = 0; v < 16; v++) acc[t][v] = acc[t][v] + T[16 * t + v] * (float)C[t][v];
+            if (bb + 1 < Q4A_BPS) {
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const float4 s4 = *reinterpret_cast<const float4 *>(d8s + Q4A_TM * bb + 32 * t + 8 * j + 4 * h);
-                    const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const float tt = dw * sv[r];
-                        acc[t][4 * j + r] = acc[t][4 * j + r] + tt * (float)C[4 * j + r];
-                    }
-                }
+                for (int t = 0; t < Q4A_MT; t++) C[t] = Cn[t];
+                T = Tn;
             }
         }
     }

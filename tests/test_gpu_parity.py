@@ -458,6 +458,34 @@ def test_actq_q4_0_tiles_bits(backend, M, N, K, row0, acc):
     w.release()
 
 
+@pytest.mark.parametrize("weights", ["moderate", "any_scale"])
+def test_actq_q4_0_scale_products_bits(backend, weights):
+    """q4_0 act-quant where the per-block scale product t = fl(d_w d8) (taken on the matrix cores as a rank-1 fp32
+    product) is subnormal or special: activation rows scaled from 1e-28 down to 1e-39 (d8 and t reaching the fp32
+    subnormal range) and one all-zero row, on moderate weight scales and on random fp16 scale bits (subnormal and
+    signed-zero d_w; NaN/Inf scales are refused when the store is made): bit-identical to quantGemmAct."""
+    M, N, K = 64, 256, 1024
+    rng = _rng(4400 + len(weights))
+    raw = (_weights(Q4, N, K, 45) if weights == "moderate" else O.random_quant(Q4, 46, N * K // 32))
+    if weights == "any_scale":  # d_w = +-0 and the smallest and largest fp16 subnormals in a few blocks
+        blk = raw.reshape(N, K // 32, 18)
+        for (n, b), bits in zip([(3, 5), (7, 0), (11, 31), (13, 2), (17, 9)], [0x8000, 0x0000, 0x0001, 0x83FF, 0x8001]):
+            blk[n, b, 0], blk[n, b, 1] = bits & 0xFF, bits >> 8
+    X = _x(rng, M * K).reshape(M, K)
+    for m in range(M):
+        X[m] *= np.float32(10.0 ** -(28 + m % 12)) if m % 4 else np.float32(1.0)
+    X[8] = 0
+    w = backend.FromQuantized(Q4, raw, N, K)
+    xb, cb = backend.ctx.to_device(X), backend.ctx.alloc(M * N * 4)
+    backend.GemmActQuant(M, N, K, xb, w, cb, accumulate=False)
+    want = O.quant_gemm_act(Q4, M, N, K, X, raw)
+    assert np.count_nonzero((np.abs(want) < np.float32(1.17549435e-38)) & (want != 0)) > 0
+    same_bits(cb.download(np.float32, M * N), want)
+    for b in (xb, cb):
+        b.free()
+    w.release()
+
+
 @pytest.mark.parametrize("dt", [Q4, Q6K])
 @pytest.mark.parametrize("N,K,M", [(14336, 4096, 512), (4096, 14336, 128)])
 def test_actq_prefill_other_dtypes_bits(backend, dt, N, K, M):
