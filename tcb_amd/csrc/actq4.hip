@@ -121,6 +121,7 @@ __global__ __launch_bounds__(Q4A_THREADS) __attribute__((amdgpu_waves_per_eu(2, 
     // weight row 32 w + lane % 32, activation rows 8 j + 4 h + r of the tile
     const int nl = lane & 31, h = lane >> 5;
     const int wrow = 32 * w + nl;
+    const int nsh = 4 * h;  // low nibbles for the lanes of k-slice 0, high for slice 1
 
     float acc[Q4A_MT][16];
 #pragma unroll
@@ -137,10 +138,8 @@ __global__ __launch_bounds__(Q4A_THREADS) __attribute__((amdgpu_waves_per_eu(2, 
         const uint32_t rw4[4] = {raw.x, raw.y, raw.z, raw.w};
         v4i B;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {  // q4 - 8 as bytes: q + 120 never carries out of a byte, xor 128
-            const uint32_t nib = h ? ((rw4[e] >> 4) & 0x0F0F0F0Fu) : (rw4[e] & 0x0F0F0F0Fu);
-            B[e] = (int)((nib + 0x78787878u) ^ 0x80808080u);
-        }
+        for (int e = 0; e < 4; e++)  // q4 - 8 as bytes: q + 120 never carries out of a byte, xor 128
+            B[e] = (int)((((rw4[e] >> nsh) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u);
         const float d8 = reinterpret_cast<const float *>(sb + L::O_D8)[Q4A_TM * bb + lane];
         const float dw = f16_to_f32(reinterpret_cast<const uint16_t *>(sb + L::O_DW)[Q4A_BPS * wrow + bb]);
         T = __builtin_amdgcn_mfma_f32_32x32x1f32(d8, dw, (v32f){0.0f}, 0, 0, 0);
