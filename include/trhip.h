@@ -243,7 +243,7 @@ int trhip_prefill_probe(trhip_ctx *ctx, int kind, int64_t M, int64_t N, int64_t 
  * refused here, never at a later GEMV. TRHIP_KNOB_KL: K-across-lanes fast GEMV (a, b, c, d) =
  * (waves, K parts, rows in flight, rows per wave); TRHIP_KNOB_FAST_Q4K: row-sliced fast q4_k GEMV
  * (blocks in flight, waves, K parts, rows per lane); TRHIP_KNOB_EXACT_ROWS: exact four-lane GEMV rows
- * per workgroup a; TRHIP_KNOB_EXACT_LANES: exact GEMV lanes per row a; TRHIP_KNOB_ACTQ_TM: act-quant
+ * per workgroup a; TRHIP_KNOB_EXACT_LANES: exact GEMV lanes per row a (4, 8 or 16); TRHIP_KNOB_ACTQ_TM: act-quant
  * MFMA row tile a (0: built-in) and, in fast mode, b K slices (0: built-in); TRHIP_KNOB_ROWS16: fast q4_k kernel for 2..16 activation rows (a, b) = (16-row tiles per
  * wave 1 or 2; K slices 1..64, clamped to the block count); TRHIP_KNOB_KL_GRID: at least a workgroups for
  * the K-across-lanes fast GEMV (its rows dealt over more, shorter row groups). */

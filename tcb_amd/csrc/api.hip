@@ -549,8 +549,8 @@ int trhip_set_launch_shape(trhip_ctx *ctx, int knob, int a, int b, int c, int d)
         ctx->force_exact_rows = a;
         return TRHIP_OK;
     case TRHIP_KNOB_EXACT_LANES:
-        if (!(reset || ((a == 4 || a == 8) && !b && !c && !d)))
-            return fail(ctx, TRHIP_ERR_INVALID, "set_launch_shape: exact lanes per row must be 4 or 8");
+        if (!(reset || ((a == 4 || a == 8 || a == 16) && !b && !c && !d)))
+            return fail(ctx, TRHIP_ERR_INVALID, "set_launch_shape: exact lanes per row must be 4, 8 or 16");
         ctx->force_exact_lanes = a;
         return TRHIP_OK;
     case TRHIP_KNOB_ACTQ_TM:

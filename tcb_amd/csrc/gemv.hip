@@ -260,16 +260,21 @@ __global__ __launch_bounds__(THREADS) void gemv_exact_kernel(const Planes p, con
     for (int l = 0; l < 8; l++) acc[l] = 0.0f;
     const float4 *xl = xs + 2 * t;
     // Loads are unconditional (clamped to the last block, re-reading it at the tail) so the ring stays
-    // in registers with static indices; only the compute is guarded, by a wave-uniform test.
-    for (int64_t b0 = 0; b0 < nb; b0 += D) {
+    // in registers with static indices. Whole rounds of D blocks run without a branch, so the LDS reads of x for
+    // several blocks are issued before their first use; the last nb % D blocks, already in the ring, follow.
+    const int64_t nfull = nb - nb % D;
+    for (int64_t b0 = 0; b0 < nfull; b0 += D) {
 #pragma unroll
         for (int s = 0; s < D; s++) {
             const int64_t b = b0 + s;
             typename B::Data cur = ring[s];
             blk.load(ring[s], (b + D < nb) ? b + D : nb - 1);
-            if (b < nb) blk.compute(acc, cur, xl + B::XSTEP * b, t);
+            blk.compute(acc, cur, xl + B::XSTEP * b, t);
         }
     }
+#pragma unroll
+    for (int s = 0; s < D; s++)
+        if (nfull + s < nb) blk.compute(acc, ring[s], xl + B::XSTEP * (nfull + s), t);
     float res = sdot32_tree(acc);
     if (live && t == 0) put_out<ACC, IO>(c, r, res);
 }
@@ -425,17 +430,240 @@ __global__ __launch_bounds__(THREADS) void gemv_exact8_kernel(const Planes p, co
 
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     const float4 *xl = xs + u;
-    for (int64_t b0 = 0; b0 < nb; b0 += D) {
+    // whole rounds of D blocks without a branch, then the last nb % D blocks from the ring (as in the four-lane
+    // kernel)
+    const int64_t nfull = nb - nb % D;
+    for (int64_t b0 = 0; b0 < nfull; b0 += D) {
 #pragma unroll
         for (int s = 0; s < D; s++) {
             const int64_t b = b0 + s;
             typename B::Data cur = ring[s];
             blk.load(ring[s], (b + D < nb) ? b + D : nb - 1);
-            if (b < nb) blk.compute(acc, cur, xl + B::XSTEP * b);
+            blk.compute(acc, cur, xl + B::XSTEP * b);
         }
     }
+#pragma unroll
+    for (int s = 0; s < D; s++)
+        if (nfull + s < nb) blk.compute(acc, ring[s], xl + B::XSTEP * (nfull + s));
     const float res = sdot32_tree8(acc);
     if (live && u == 0) put_out<ACC, IO>(c, r, res);
+}
+
+// ---------------------------------------------------------------- sixteen lanes per row
+// For stores whose rows alone leave SIMDs idle (4096 rows x 8 lanes is 512 waves for 1024 SIMDs): lane v (0..15)
+// owns the two chains 2v, 2v+1 (lanes 2(v&3), 2(v&3)+1 of sdot32 register v>>2), i.e. elements 32G + 2v, 2v+1 of
+// every 32-element group G in ascending G. The row's 16 lanes read the block's 16 (q4_0) or 32 (q8_0) code bytes as
+// one contiguous piece, two bytes per lane (q4_k: four 2-byte pieces per block, one per group pair; q6_k: the
+// eight-lane pieces split in two). The tree: A0+A1 and A2+A3 by xor-shuffle 4, their sum (Y) by xor 8,
+// s_l = Y[l] + Y[l+4] by xor 2, (s0+s2) and (s1+s3) by xor 1, their sum in-lane; IEEE addition is commutative,
+// so the partners of every shuffle hold identical bits.
+// VOL: hide the codes with a volatile statement, which also keeps the loads in program order around it (faster for
+// the q8_0 / q4_0 blocks, two elements per lane: 4096x14336 30.4 against 32.2 us)
+template <bool VOL>
+__device__ __forceinline__ void fma2(float *acc, uint32_t codes, float s, float negm, float2 xv) {
+    codes = VOL ? opaque(codes) : hide(codes);
+    acc[0] = fmaf(fmaf(s, ubyte_f(codes, 0), negm), xv.x, acc[0]);
+    acc[1] = fmaf(fmaf(s, ubyte_f(codes, 1), negm), xv.y, acc[1]);
+}
+
+template <int DT>
+struct Blk16;
+
+template <>
+struct Blk16<kQ8> {
+    static constexpr int DEPTH = 24;
+    struct Data { uint32_t q, d; };
+    const uint16_t *qp;
+    const uint16_t *dp;
+    __device__ Blk16(const Planes &p, int64_t row, int v)
+        : qp(reinterpret_cast<const uint16_t *>(p.qs + row * p.nb * 32) + v), dp(p.d + row * p.nb) {}
+    __device__ __forceinline__ void load(Data &v, int64_t b) const { v.q = qp[16 * b]; v.d = dp[b]; }
+    __device__ __forceinline__ void compute(float *acc, const Data &v, const float2 *xb) const {
+        const float d = f16_to_f32((uint16_t)v.d);
+        fma2<true>(acc, v.q ^ 0x8080u, d, -128.0f * d, xb[0]);  // (u - 128)*d exact
+    }
+    static constexpr int XSTEP = 16;  // float2s of x per block
+};
+
+template <>
+struct Blk16<kQ4> {
+    static constexpr int DEPTH = 24;
+    struct Data { uint32_t q, d; };
+    const uint16_t *qp;
+    const uint16_t *dp;
+    int sh;
+    __device__ Blk16(const Planes &p, int64_t row, int v)
+        : qp(reinterpret_cast<const uint16_t *>(p.qs + row * p.nb * 16) + (v & 7)), dp(p.d + row * p.nb),
+          sh(v >= 8 ? 4 : 0) {}  // lanes 8..15 take the high nibbles (elements 16..31)
+    __device__ __forceinline__ void load(Data &v, int64_t b) const { v.q = qp[8 * b]; v.d = dp[b]; }
+    __device__ __forceinline__ void compute(float *acc, const Data &v, const float2 *xb) const {
+        const float d = f16_to_f32((uint16_t)v.d);
+        fma2<true>(acc, (v.q >> sh) & 0x0F0Fu, d, -8.0f * d, xb[0]);
+    }
+    static constexpr int XSTEP = 16;
+};
+
+template <>
+struct Blk16<kQ4K> {
+    static constexpr int DEPTH = 6;
+    struct Data { uint4 h; uint32_t q[4]; };
+    const uint4 *hp;
+    // lane v's two code bytes of group pair g (elements 2v, 2v+1 of sub-blocks 2g and 2g+1) in the lane-sliced qs
+    // plane: byte 64((v>>2)>>1) + 16g + 8((v>>2)&1) + 2(v&3)
+    const uint16_t *qp;
+    __device__ Blk16(const Planes &p, int64_t row, int v)
+        : hp(reinterpret_cast<const uint4 *>(p.aux + row * p.nb * 16)),
+          qp(reinterpret_cast<const uint16_t *>(p.qs + row * p.nb * 128) + 32 * (v >> 3) + 4 * ((v >> 2) & 1) + (v & 3)) {}
+    __device__ __forceinline__ void load(Data &v, int64_t b) const {
+        v.h = hp[b];
+#pragma unroll
+        for (int g = 0; g < 4; g++) v.q[g] = qp[64 * b + 8 * g];
+    }
+    __device__ __forceinline__ void compute(float *acc, const Data &v, const float2 *xb) const {
+        const float d = f16_to_f32((uint16_t)(v.h.x & 0xFFFF)), dmin = f16_to_f32((uint16_t)(v.h.x >> 16));
+        const float d16 = d * 0.0625f;
+        uint32_t sc_lo, sc_hi, m_lo, m_hi;
+        q4k_scales(v.h.y, v.h.z, v.h.w, sc_lo, sc_hi, m_lo, m_hi);
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const uint32_t scw = g < 2 ? sc_lo : sc_hi, mw = g < 2 ? m_lo : m_hi;
+            const int k0 = (2 * g) & 3, k1 = (2 * g + 1) & 3;
+            const float s0 = d * ubyte_f(scw, k0), n0 = -(dmin * ubyte_f(mw, k0));
+            const float s1 = d16 * ubyte_f(scw, k1), n1 = -(dmin * ubyte_f(mw, k1));
+            // sub-block 2g: low nibbles; sub-block 2g+1: high nibbles read as 16*code with scale d/16 (exact)
+            fma2<false>(acc, v.q[g] & 0x0F0Fu, s0, n0, xb[16 * (2 * g)]);
+            fma2<false>(acc, v.q[g] & 0xF0F0u, s1, n1, xb[16 * (2 * g + 1)]);
+        }
+    }
+    static constexpr int XSTEP = 128;
+};
+
+template <>
+struct Blk16<kQ6K> {
+    static constexpr int DEPTH = 4;
+    struct Data { uint32_t l[4], hq[2]; uint4 sv; uint32_t d; };
+    // lane v's elements 2v, 2v+1 sit in the two bytes at 2(v&1) of the eight-lane kernel's 4-byte pieces of lane
+    // v>>1: ql bytes 32(v>>2) + 4((v>>1)&1) + 2(v&1) + 16n + 8h, qh bytes 16(v>>2) + 4((v>>1)&1) + 2(v&1) + 8n
+    const uint16_t *lp, *hp;
+    const uint4 *sp;
+    const uint16_t *dp;
+    int th;
+    __device__ Blk16(const Planes &p, int64_t row, int v)
+        : lp(reinterpret_cast<const uint16_t *>(p.qs + row * p.nb * 128) + 16 * (v >> 2) + 2 * ((v >> 1) & 1) + (v & 1)),
+          hp(reinterpret_cast<const uint16_t *>(p.aux + row * p.nb * 64) + 8 * (v >> 2) + 2 * ((v >> 1) & 1) + (v & 1)),
+          sp(reinterpret_cast<const uint4 *>(p.sc + row * p.nb * 16)), dp(p.d + row * p.nb), th(v >> 3) {}
+    __device__ __forceinline__ void load(Data &v, int64_t b) const {
+#pragma unroll
+        for (int i = 0; i < 4; i++) v.l[i] = lp[64 * b + 4 * i];  // i = 2n + h
+#pragma unroll
+        for (int n = 0; n < 2; n++) v.hq[n] = hp[32 * b + 4 * n];
+        v.sv = sp[b];
+        v.d = dp[b];
+    }
+    __device__ __forceinline__ void compute(float *acc, const Data &v, const float2 *xb) const {
+        const float d = f16_to_f32((uint16_t)v.d);
+        const uint32_t scw[4] = {v.sv.x, v.sv.y, v.sv.z, v.sv.w};
+#pragma unroll
+        for (int n = 0; n < 2; n++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t A = v.l[2 * n + (k & 1)];
+                const uint32_t nib = (k < 2) ? (A & 0x0F0Fu) : ((A >> 4) & 0x0F0Fu);
+                const uint32_t code = nib | (((v.hq[n] >> (2 * k)) & 0x0303u) << 4);
+                const int si = 8 * n + 2 * k + th;  // 16-element scale of elements 2v, 2v+1 of group 4n + k
+                const int8_t scv = (int8_t)((scw[si >> 2] >> (8 * (si & 3))) & 0xFF);
+                const float ds = d * (float)scv;  // exact (11 x 8 bits)
+                // fl(ds*(code-32)) == fmaf(ds, code, -32*ds): same real number, one rounding
+                fma2<false>(acc, code, ds, -32.0f * ds, xb[16 * (4 * n + k)]);
+            }
+    }
+    static constexpr int XSTEP = 128;
+};
+
+__device__ __forceinline__ float sdot32_tree16(const float *acc) {
+    float e[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const float a = acc[i] + __shfl_xor(acc[i], 4);  // A0+A1 (lanes 0-7), A2+A3 (lanes 8-15) at l = 2(v&3) + i
+        const float y = a + __shfl_xor(a, 8);            // Y[2(v&3) + i]
+        const float sl = y + __shfl_xor(y, 2);           // s_i (v&3 = 0, 2) or s_{2+i} (v&3 = 1, 3)
+        e[i] = sl + __shfl_xor(sl, 1);                   // s_i + s_{2+i}
+    }
+    return e[0] + e[1];  // (s0+s2) + (s1+s3)
+}
+
+template <int DT, bool ACC, int THREADS, int IO>
+__device__ __forceinline__ void exact16_body(const Planes p, const void *__restrict__ x, void *__restrict__ c, int64_t N,
+                                             int64_t row0, int64_t K) {
+    extern __shared__ float4 xs[];  // K / 4 float4: the whole activation vector
+    const int v = threadIdx.x & 15;
+    const int64_t r = (int64_t)blockIdx.x * (THREADS / 16) + (threadIdx.x >> 4);
+    const bool live = r < N;
+    const int64_t row = row0 + (live ? r : 0);
+    const int64_t nb = p.nb;
+    using B = Blk16<DT>;
+    constexpr int D = B::DEPTH;
+    B blk(p, row, v);
+    typename B::Data ring[D];
+    XStager<THREADS, IO> xst;
+    xst.issue(x, K / 4, 0);
+    __builtin_amdgcn_sched_barrier(0);  // x is requested first: the wait before its stores then skips the weights
+#pragma unroll
+    for (int s = 0; s < D; s++) blk.load(ring[s], s < nb ? s : nb - 1);
+    xst.commit(xs, K / 4, 0);
+    xst.rest(xs, x, K / 4);
+    __syncthreads();
+
+    float acc[2] = {0.0f, 0.0f};
+    const float2 *xl = reinterpret_cast<const float2 *>(xs) + v;
+    // whole rounds of D blocks without a branch, then the last nb % D blocks from the ring (as in the four-lane
+    // kernel)
+    const int64_t nfull = nb - nb % D;
+    for (int64_t b0 = 0; b0 < nfull; b0 += D) {
+#pragma unroll
+        for (int s = 0; s < D; s++) {
+            const int64_t b = b0 + s;
+            typename B::Data cur = ring[s];
+            blk.load(ring[s], (b + D < nb) ? b + D : nb - 1);
+            blk.compute(acc, cur, xl + B::XSTEP * b);
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < D; s++)
+        if (nfull + s < nb) blk.compute(acc, ring[s], xl + B::XSTEP * (nfull + s));
+    const float res = sdot32_tree16(acc);
+    if (live && v == 0) put_out<ACC, IO>(c, r, res);
+}
+
+template <int DT, bool ACC, int THREADS, int IO = TRHIP_F32>
+__global__ __launch_bounds__(THREADS) void gemv_exact16_kernel(const Planes p, const void *__restrict__ x,
+                                                               void *__restrict__ c, int64_t N, int64_t row0, int64_t K) {
+    exact16_body<DT, ACC, THREADS, IO>(p, x, c, N, row0, K);
+}
+
+// The same with the register budget of one wave per SIMD, for grids of at most one wave per SIMD: the compiler then
+// issues a block's LDS reads of x ahead of their use instead of waiting for each (q4_k 4096x14336 26.3 -> 22.2 us,
+// 4096x4096 9.45 -> 8.39; q6_k 4096x14336 28.6 -> 24.6).
+template <int DT, bool ACC, int THREADS, int IO = TRHIP_F32>
+__global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemv_exact16w1_kernel(
+    const Planes p, const void *__restrict__ x, void *__restrict__ c, int64_t N, int64_t row0, int64_t K) {
+    exact16_body<DT, ACC, THREADS, IO>(p, x, c, N, row0, K);
+}
+
+template <int DT, int THREADS, int MINW>
+void launch_exact16_t(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N, const void *x, void *c,
+                      bool acc, size_t lds, int io) {
+    dim3 grid((unsigned)((N + THREADS / 16 - 1) / (THREADS / 16))), block(THREADS);
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, block, lds, ctx->stream, w->planes(), x, c, N, row0, w->K); };
+    if constexpr (MINW == 1) {
+        if (io == TRHIP_F16) acc ? go(gemv_exact16w1_kernel<DT, true, THREADS, TRHIP_F16>) : go(gemv_exact16w1_kernel<DT, false, THREADS, TRHIP_F16>);
+        else if (io == TRHIP_BF16) acc ? go(gemv_exact16w1_kernel<DT, true, THREADS, TRHIP_BF16>) : go(gemv_exact16w1_kernel<DT, false, THREADS, TRHIP_BF16>);
+        else acc ? go(gemv_exact16w1_kernel<DT, true, THREADS>) : go(gemv_exact16w1_kernel<DT, false, THREADS>);
+    } else {
+        if (io == TRHIP_F16) acc ? go(gemv_exact16_kernel<DT, true, THREADS, TRHIP_F16>) : go(gemv_exact16_kernel<DT, false, THREADS, TRHIP_F16>);
+        else if (io == TRHIP_BF16) acc ? go(gemv_exact16_kernel<DT, true, THREADS, TRHIP_BF16>) : go(gemv_exact16_kernel<DT, false, THREADS, TRHIP_BF16>);
+        else acc ? go(gemv_exact16_kernel<DT, true, THREADS>) : go(gemv_exact16_kernel<DT, false, THREADS>);
+    }
 }
 
 template <int DT, int THREADS>
@@ -476,8 +704,25 @@ int launch_exact(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N,
     // q8_0 (4096x4096: 20.3 vs 23.6) and equal for q4_0; for q6_k 4 stays faster on large grids (14336x4096: 17.8 vs
     // 19.9 us, 128256x4096: 109 vs 139) and 8 wins below 10240 rows (1024x4096 15.0 -> 10.9, 4096x4096 15.5 -> 11.2,
     // 4096x14336 47.7 -> 34.5; bit-identical). trhip_set_launch_shape(TRHIP_KNOB_EXACT_LANES) overrides.
-    const int lanes = ctx->force_exact_lanes ? ctx->force_exact_lanes : (DT == kQ6K && N >= 10240 ? 4 : 8);
-    if (lanes == 8) {
+    // 16 lanes below 10240 rows, where 8 leave SIMDs idle (cold, us, 8 -> 16 lanes, bit-identical: q4_k 4096x14336
+    // 32.9 -> 26.3, 4096x4096 11.0 -> 9.4; q6_k 4096x14336 34.9 -> 28.6; q4_0 4096x14336 41.3 -> 30.4; q8_0
+    // 4096x4096 15.0 -> 12.0); from 10240 rows 16 lanes are slower (q4_k 14336x4096 13.6 -> 16.0).
+    const int lanes = ctx->force_exact_lanes ? ctx->force_exact_lanes : N < 10240 ? 16 : (DT == kQ6K ? 4 : 8);
+    if (lanes == 16) {
+        // rows per workgroup: the most (16, 8, 4) that still give 256 workgroups; the k-quants take the one-wave
+        // register budget up to 4096 rows (at most 1024 waves; 6144x4096 measured 10.8 -> 15.1 us with it), q8_0 and
+        // q4_0 never (4096x14336: 30.4 -> 32.4 us)
+        constexpr bool kq = DT == kQ4K || DT == kQ6K;
+        if (N > 4096 || !kq) {
+            if (N >= 16 * 256) launch_exact16_t<DT, 256, 4>(ctx, w, row0, N, x, c, acc, lds, io);
+            else if (N >= 8 * 256) launch_exact16_t<DT, 128, 4>(ctx, w, row0, N, x, c, acc, lds, io);
+            else launch_exact16_t<DT, 64, 4>(ctx, w, row0, N, x, c, acc, lds, io);
+        } else if (N >= 16 * 256) launch_exact16_t<DT, 256, 1>(ctx, w, row0, N, x, c, acc, lds, io);
+        else if (N >= 8 * 256) launch_exact16_t<DT, 128, 1>(ctx, w, row0, N, x, c, acc, lds, io);
+        else launch_exact16_t<DT, 64, 1>(ctx, w, row0, N, x, c, acc, lds, io);
+        return launch_check(ctx, "gemv_exact16");
+    }
+    if (lanes >= 8) {
         // 8 lanes per row: 32 rows per 256-thread workgroup, 16 per 128-thread one and 8 per 64-thread one as N falls
         // (cold, us, 128 -> 64 threads, bit-identical: q4_k 1024x4096 11.0 -> 10.66, 2048x4096 11.1 -> 10.8,
         // 1024x14336 33.6 -> 32.1; q8_0 / q4_0 1024x4096 18.3 / 18.1 -> 17.9 / 17.2); q4_k keeps 16 rows per workgroup

@@ -99,6 +99,13 @@ __device__ __forceinline__ uint32_t opaque(uint32_t v) {
     asm volatile("" : "+v"(v));
     return v;
 }
+// The same without volatile: the value stays hidden, but the (empty) statement has no side effects, so the
+// scheduler may still move loads across it (a volatile one keeps every LDS read of a loop body in program order,
+// each waited for where it is used).
+__device__ __forceinline__ uint32_t hide(uint32_t v) {
+    asm("" : "+v"(v));
+    return v;
+}
 
 // Global -> LDS copies (buffer_load ... lds) issued as inline assembly. The compiler's waitcnt pass, when it sees
 // an LDS-DMA request in flight, makes every later LDS access it cannot prove disjoint from the request's destination
@@ -323,7 +330,7 @@ struct trhip_ctx {
     int kl_min_wgs = 0;         // K-across-lanes GEMV: at least this many workgroups (0: built-in)
     int force_fast_q4k = 0;     // row-sliced fast q4_k GEMV: 1000 D + 100 WAVES + 10 KS + R
     int force_exact_rows = 0;   // exact four-lane GEMV rows per workgroup (16, 32, 64)
-    int force_exact_lanes = 0;  // exact GEMV lanes per row (4, 8)
+    int force_exact_lanes = 0;  // exact GEMV lanes per row (4, 8, 16)
     int force_actq_tm = 0;      // act-quant MFMA row tile (32, 64)
     int force_actq_slices = 0;  // act-quant MFMA K slices, fast mode (0: built-in)
     int force_rows16 = 0;       // batched-decode q4_k kernel: 100 tiles per wave + K slices

@@ -13,7 +13,7 @@ import pytest
 import oracle as O
 from conftest import rel_err, same_bits
 from tcb_amd import BLOCK, MODE_EXACT, MODE_FAST, Q4, Q4K, Q6K, Q8, TrhipError
-from tcb_amd._lib import KNOB_ACTQ_TM, KNOB_KL
+from tcb_amd._lib import KNOB_ACTQ_TM, KNOB_EXACT_LANES, KNOB_KL
 from tcb_amd import synth
 
 pytestmark = pytest.mark.gpu
@@ -185,6 +185,18 @@ def test_gemv_set_slice_unaligned(backend, dt):
     got, want = _gemv_case(backend, dt, 50, K, seed=8, row0=10, rows=20)
     same_bits(got, want)
     got, want = _gemv_case(backend, dt, 50, K, seed=9, x_off=4)
+    same_bits(got, want)
+
+
+@pytest.mark.parametrize("dt", DTS)
+@pytest.mark.parametrize("lanes", [4, 8, 16])
+@pytest.mark.parametrize("N,Kb", [(5, 7), (33, 25), (300, 40), (4096, 3)])
+def test_gemv_exact_lanes_bits(backend, launch_shape, dt, lanes, N, Kb):
+    """Every lane count of the exact GEMV (4, 8 or 16 lanes per row, each lane owning 8, 4 or 2 of the 32 sdot32
+    chains; 16 lanes with the one-wave register budget up to 4096 rows for the k-quants) on block counts that leave
+    0 .. ring-depth - 1 blocks after the last whole round, x1 and x1000: bit-identical to quantDot."""
+    launch_shape(KNOB_EXACT_LANES, lanes)
+    got, want = _gemv_case(backend, dt, N, Kb * BLOCK[dt][0], seed=N + Kb + lanes, scale=1000.0 if N == 33 else 1.0)
     same_bits(got, want)
 
 
