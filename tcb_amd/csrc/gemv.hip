@@ -260,7 +260,7 @@ __global__ __launch_bounds__(THREADS) void gemv_exact_kernel(const Planes p, con
     for (int l = 0; l < 8; l++) acc[l] = 0.0f;
     const float4 *xl = xs + 2 * t;
     // Loads are unconditional (clamped to the last block, re-reading it at the tail) so the ring stays
-    // in registers with static indices. Whole rounds of D blocks run without a branch, so the LDS reads of x for
+    // in registers with static indices. Full passes of the D-block ring run without a branch, so the LDS reads of x for
     // several blocks are issued before their first use; the last nb % D blocks, already in the ring, follow.
     const int64_t nfull = nb - nb % D;
     for (int64_t b0 = 0; b0 < nfull; b0 += D) {
@@ -430,7 +430,7 @@ __global__ __launch_bounds__(THREADS) void gemv_exact8_kernel(const Planes p, co
 
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     const float4 *xl = xs + u;
-    // whole rounds of D blocks without a branch, then the last nb % D blocks from the ring (as in the four-lane
+    // full passes of the D-block ring without a branch, then the last nb % D blocks from the ring (as in the four-lane
     // kernel)
     const int64_t nfull = nb - nb % D;
     for (int64_t b0 = 0; b0 < nfull; b0 += D) {
@@ -616,7 +616,7 @@ __device__ __forceinline__ void exact16_body(const Planes p, const void *__restr
 
     float acc[2] = {0.0f, 0.0f};
     const float2 *xl = reinterpret_cast<const float2 *>(xs) + v;
-    // whole rounds of D blocks without a branch, then the last nb % D blocks from the ring (as in the four-lane
+    // full passes of the D-block ring without a branch, then the last nb % D blocks from the ring (as in the four-lane
     // kernel)
     const int64_t nfull = nb - nb % D;
     for (int64_t b0 = 0; b0 < nfull; b0 += D) {
