@@ -190,10 +190,11 @@ def test_gemv_set_slice_unaligned(backend, dt):
 
 @pytest.mark.parametrize("dt", DTS)
 @pytest.mark.parametrize("lanes", [4, 8, 16])
-@pytest.mark.parametrize("N,Kb", [(5, 7), (33, 25), (300, 40), (4096, 3)])
+@pytest.mark.parametrize("N,Kb", [(5, 7), (33, 25), (300, 40), (2100, 9), (4096, 3)])
 def test_gemv_exact_lanes_bits(backend, launch_shape, dt, lanes, N, Kb):
     """Every lane count of the exact GEMV (4, 8 or 16 lanes per row, each lane owning 8, 4 or 2 of the 32 sdot32
-    chains; 16 lanes with the one-wave register budget up to 4096 rows for the k-quants) on block counts that leave
+    chains; 16 lanes in workgroups of 4, 8 or 16 rows, with the one-wave register budget up to 4096 rows for the
+    k-quants) on block counts that leave
     0 .. ring-depth - 1 blocks after the last full pass of the ring, x1 and x1000: bit-identical to quantDot."""
     launch_shape(KNOB_EXACT_LANES, lanes)
     got, want = _gemv_case(backend, dt, N, Kb * BLOCK[dt][0], seed=N + Kb + lanes, scale=1000.0 if N == 33 else 1.0)
