@@ -704,10 +704,16 @@ int launch_exact(trhip_ctx *ctx, const trhip_wstore *w, int64_t row0, int64_t N,
     // q8_0 (4096x4096: 20.3 vs 23.6) and equal for q4_0; for q6_k 4 stays faster on large grids (14336x4096: 17.8 vs
     // 19.9 us, 128256x4096: 109 vs 139) and 8 wins below 10240 rows (1024x4096 15.0 -> 10.9, 4096x4096 15.5 -> 11.2,
     // 4096x14336 47.7 -> 34.5; bit-identical). trhip_set_launch_shape(TRHIP_KNOB_EXACT_LANES) overrides.
-    // 16 lanes below 10240 rows, where 8 leave SIMDs idle (cold, us, 8 -> 16 lanes, bit-identical: q4_k 4096x14336
-    // 32.9 -> 26.3, 4096x4096 11.0 -> 9.4; q6_k 4096x14336 34.9 -> 28.6; q4_0 4096x14336 41.3 -> 30.4; q8_0
-    // 4096x4096 15.0 -> 12.0); from 10240 rows 16 lanes are slower (q4_k 14336x4096 13.6 -> 16.0).
-    const int lanes = ctx->force_exact_lanes ? ctx->force_exact_lanes : N < 10240 ? 16 : (DT == kQ6K ? 4 : 8);
+    // 16 lanes up to 48 rows per CU (12288 on 256 CUs: at most three 16-row workgroups per CU), where 8 leave SIMDs
+    // idle or 16 still balance (cold, us, 8 -> 16 lanes, bit-identical: q4_k 4096x14336 32.9 -> 26.3, 4096x4096
+    // 11.0 -> 9.4, 12288x4096 13.2 -> 12.9; q6_k 4096x14336 34.9 -> 28.6, 10240x4096 19.3 -> 14.6; q4_0 4096x14336
+    // 41.3 -> 30.4; q8_0 4096x4096 15.0 -> 12.0). Above that a fourth workgroup lands on some CUs and 16 lanes lose
+    // (q4_k 13312x4096 13.7 -> 15.5, 14336x4096 14.1 -> 15.9), except q8_0 from 80 rows per CU (20480x4096 32.3 ->
+    // 29.4, 28672x4096 48.7 -> 37.5). q6_k keeps 4 lanes on large grids (128256x4096: 117 against 130 on 16).
+    const int64_t cus = ctx->sm_count > 0 ? ctx->sm_count : 256;
+    const int lanes = ctx->force_exact_lanes ? ctx->force_exact_lanes
+                      : (N <= 48 * cus || (DT == kQ8 && N >= 80 * cus)) ? 16
+                      : (DT == kQ6K ? 4 : 8);
     if (lanes == 16) {
         // rows per workgroup: the most (16, 8, 4) that still give 256 workgroups; the k-quants take the one-wave
         // register budget up to 4096 rows (at most 1024 waves; 6144x4096 measured 10.8 -> 15.1 us with it), q8_0 and
